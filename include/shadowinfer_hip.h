@@ -1,0 +1,221 @@
+/*
+ * shadowinfer_hip.h — C ABI of the MI355X (gfx950) quantized data plane.
+ *
+ * One shared library, libshadowinfer_hip.so, exports these entry points. They
+ * replace the torch op chains of the reference's hot path (cited per entry as
+ * file:line in ShadowInfer). Conventions:
+ *
+ *  - Every pointer argument named for data is a DEVICE pointer unless the
+ *    comment says "host". Tables of bucket pointers (`buckets`) are HOST
+ *    arrays of 16 device pointers: buckets[4*p + j], p = precision code
+ *    (0 fp32, 1 fp16, 2 int8, 3 int4), j = 0 k, 1 v, 2 scale_k, 3 scale_v.
+ *    Entries for absent buckets may be NULL.
+ *  - Bucket memory uses the reference's tensor layouts exactly
+ *    (shadowinfer/shadowkv/packed_kv_cache.py:137-218):
+ *      fp32/fp16 : k,v [n, B, D]
+ *      int8      : k,v [n, B, D] int8, scale [n, B, 1] in the input dtype
+ *      int4      : k,v [n * ceil(B*D/2)] uint8 (offset-binary nibbles,
+ *                  high nibble first), scale [n*B, D/g, 1] in the input dtype
+ *    where n is the number of entries of that precision, ordered token-major.
+ *  - Entries are token-heads; entry id e = t * H + h (token-major), which is
+ *    the row-major flat index of the int8 [S, H] precision-code matrix.
+ *  - The caller allocates every output and workspace. The library keeps no
+ *    device allocations between calls and is reentrant; work is ordered on
+ *    the given stream (a hipStream_t; NULL = the default stream).
+ *  - Return value: 0 on success, non-zero on failure; si_last_error() then
+ *    returns a thread-local message. Errors never fall back to other code.
+ */
+#ifndef SHADOWINFER_HIP_H
+#define SHADOWINFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SI_ABI_VERSION 1
+
+#define SI_OK 0
+#define SI_ERR_INVALID 1
+#define SI_ERR_HIP 2
+#define SI_ERR_UNSUPPORTED 3
+
+/* Element dtypes */
+#define SI_DT_F32 0
+#define SI_DT_F16 1
+#define SI_DT_BF16 2
+
+/* Precision codes: shadowinfer/shadowkv/precision_plan.py:20-26 */
+#define SI_PREC_FP32 0
+#define SI_PREC_FP16 1
+#define SI_PREC_INT8 2
+#define SI_PREC_INT4 3
+#define SI_PREC_EVICTED 4
+
+typedef void* si_stream_t;
+
+/* Version of this ABI (SI_ABI_VERSION). No reference counterpart. */
+int si_abi_version(void);
+
+/* Thread-local text of the last failure (empty string if none). Replaces the
+ * TORCH_CHECK messages of shadowinfer/kernels/cpp/quantize_int4.cu:176-177. */
+const char* si_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* Precision plan                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Bytes of device workspace si_plan_scan needs for n_entries entries. */
+size_t si_plan_workspace_bytes(int64_t n_entries);
+
+/* Replaces the grouping of PrecisionPlan.from_codes
+ * (shadowinfer/shadowkv/precision_plan.py:136-151) and of the evict
+ * bookkeeping (shadowinfer/shadowkv/packed_kv_cache.py:679-737).
+ * codes     : int8 [n_entries] (token-major); values outside 0..4 are absent
+ * evict_mask: optional uint8 [n_entries]; non-zero forces a present entry absent
+ * out_code  : int8 [n_entries], sanitized code (absent -> 4)
+ * out_slot  : int32 [n_entries], position of the entry in its precision bucket
+ *             (entries of one precision keep token-major order); -1 if absent
+ * out_counts: int64 [5] device, entries per code 0..4 */
+int si_plan_scan(const int8_t* codes, const uint8_t* evict_mask, int64_t n_entries,
+                 int8_t* out_code, int32_t* out_slot, int64_t* out_counts,
+                 void* workspace, size_t workspace_bytes, si_stream_t stream);
+
+/* Replaces the flat-index build of PrecisionPlan.from_codes
+ * (precision_plan.py:144-151): for each present entry e = t*H + h of code p,
+ * flat_out[p][slot] = h*S + t (int64) and entry_out[p][slot] = e (int32).
+ * flat_out / entry_out: HOST arrays of 4 device pointers (NULL to skip). */
+int si_plan_scatter(const int8_t* code, const int32_t* slot, int64_t S, int64_t H,
+                    int64_t* const* flat_out, int32_t* const* entry_out,
+                    si_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Packed KV cache                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces PackedKVCache._do_pack_with_plan (packed_kv_cache.py:222-365),
+ * including Quantizer.quantize_int8/int4 (utils/quantization.py:120-178) and
+ * _pack_int4_rows (packed_kv_cache.py:367-388).
+ * k, v: [B, H, S, D] contiguous, dtype SI_DT_*; group: effective int4 group
+ * size (must divide D); code/slot: from si_plan_scan. Writes every bucket. */
+int si_kv_pack(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+               int64_t D, int64_t group, const int8_t* code, const int32_t* slot,
+               void* const* buckets, si_stream_t stream);
+
+/* Replaces PackedKVCache.unpack (packed_kv_cache.py:535-577) and
+ * _dequantize_int4_bucket (636-656). Writes every element of out_k/out_v
+ * ([B, H, S, D] fp32), absent entries as +0.0. scale_dtype: dtype of the
+ * stored scales. */
+int si_kv_unpack(const int8_t* code, const int32_t* slot, const void* const* buckets,
+                 int scale_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                 int64_t group, float* out_k, float* out_v, si_stream_t stream);
+
+/* Replaces the copy loop of PackedKVCache.apply_reuse_mask
+ * (packed_kv_cache.py:791-852). For each present entry (t,h) of the current
+ * cache with mask[t*H+h] != 0: if t < S_prev and the previous cache holds it
+ * with the same precision, its data row and scale row(s) are copied from the
+ * previous bucket; if the previous cache holds it with another precision,
+ * stats[1] is incremented. stats (optional, int64 [2] device, zeroed by the
+ * caller): applied, skipped_precision. */
+int si_kv_reuse(const int8_t* cur_code, const int32_t* cur_slot, void* const* cur_buckets,
+                int64_t S, const int8_t* prev_code, const int32_t* prev_slot,
+                const void* const* prev_buckets, int64_t S_prev, const uint8_t* mask,
+                int64_t H, int64_t B, int64_t D, int64_t group, int scale_dtype,
+                int64_t* stats, si_stream_t stream);
+
+/* Replaces the index_select compaction of PackedKVCache.evict
+ * (packed_kv_cache.py:698-737): every entry present in new_code is copied from
+ * old bucket row old_slot to new bucket row new_slot (same precision). */
+int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
+                  const void* const* old_buckets, const int8_t* new_code,
+                  const int32_t* new_slot, void* const* new_buckets, int64_t n_entries,
+                  int64_t B, int64_t D, int64_t group, int scale_dtype, si_stream_t stream);
+
+/* Replaces unpack() -> softmax(q k^T * sm_scale) v with no mask
+ * (shadowinfer/models/simple_diffusion_llm.py:165-169) as one fused kernel
+ * that dequantizes packed K/V tiles into LDS; the dense K/V never exist.
+ * Semantic neighbour of shadowinfer/kernels/__init__.py:473-537.
+ * q, out: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16; D = 64 or 128. */
+int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
+                       int64_t D, const int8_t* code, const int32_t* slot,
+                       const void* const* buckets, int scale_dtype, int64_t S_kv,
+                       int64_t group, float sm_scale, void* out, si_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Quantizer                                                               */
+/* ---------------------------------------------------------------------- */
+
+/* Quantizer.quantize_int8 over rows of D (utils/quantization.py:120-142).
+ * q: int8 [rows, D]; scale: [rows] in dtype. */
+int si_quant_rows_i8(const void* x, int dtype, int64_t rows, int64_t D, int8_t* q,
+                     void* scale, si_stream_t stream);
+
+/* Quantizer.quantize_int4 (utils/quantization.py:144-178).
+ * q: int8 [rows, D]; scale: [rows, D/group] in dtype. */
+int si_quant_rows_i4(const void* x, int dtype, int64_t rows, int64_t D, int64_t group,
+                     int8_t* q, void* scale, si_stream_t stream);
+
+/* _pack_int4_rows (packed_kv_cache.py:367-388) / Quantizer.pack_int4
+ * (utils/quantization.py:248-277) / kernels._pack_int4 (kernels/__init__.py:
+ * 382-402): rows of L int8 codes -> rows of ceil(L/2) bytes. */
+int si_int4_pack_rows(const int8_t* q, int64_t rows, int64_t L, uint8_t* out,
+                      si_stream_t stream);
+
+/* Quantizer.unpack_int4 (utils/quantization.py:279-318) / kernels._unpack_int4
+ * (kernels/__init__.py:405-420): rows of row_bytes bytes -> rows of L codes. */
+int si_int4_unpack_rows(const uint8_t* in, int64_t rows, int64_t row_bytes, int64_t L,
+                        int8_t* out, si_stream_t stream);
+
+/* Quantizer.dequantize_int8 / dequantize_int4 (utils/quantization.py:180-219):
+ * out[r, d] = float(q[r, d]) * float(scale[r, d / group]). */
+int si_dequant_rows(const int8_t* q, const void* scale, int scale_dtype, int64_t rows,
+                    int64_t D, int64_t group, float* out, si_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* INT8 FFN linear                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* INT8Linear.from_linear (ffn_optimizer/int8_linear.py:65-82):
+ * w fp32 [N, K] -> qweight int8 [K, N] (transposed), scale fp32 [N]. */
+int si_weight_quant_i8(const float* w, int64_t N, int64_t K, int8_t* qweight,
+                       float* scale, si_stream_t stream);
+
+/* INT8Linear.forward prologue (int8_linear.py:96-98): per-row dynamic
+ * symmetric int8, clamp +-127, scale floor 1e-8. x [M, K] in dtype. */
+int si_act_quant_i8(const void* x, int dtype, int64_t M, int64_t K, int8_t* q,
+                    float* scale, si_stream_t stream);
+
+/* Bytes of device workspace the GEMM entry points need for this shape (split-K
+ * partial sums; 0 when the shape runs without splitting). */
+size_t si_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* torch._int_mm (int8_linear.py:102): a int8 [M, K] x b int8 [K, N] ->
+ * c int32 [M, N], exact. */
+int si_gemm_i8i8_i32(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K,
+                     int32_t* c, void* workspace, size_t workspace_bytes, si_stream_t stream);
+
+/* _int_mm + epilogue (int8_linear.py:102-115): out[m, n] =
+ * T(float(acc) * (sx[m] * sw[n]) [+ bias[n]]), T = out_dtype. bias optional. */
+int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t* b, const float* sw,
+                       const float* bias, int64_t M, int64_t N, int64_t K, void* out,
+                       int out_dtype, void* workspace, size_t workspace_bytes,
+                       si_stream_t stream);
+
+/* Workspace bytes of si_int8_linear_forward (quantized activations, their
+ * scales and the GEMM workspace). */
+size_t si_int8_linear_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
+/* Whole INT8Linear.forward on a 2-D input (int8_linear.py:88-115):
+ * activation quantization, int8 GEMM, epilogue. out [M, N] in dtype. */
+int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64_t N,
+                           const int8_t* qweight, const float* sw, const float* bias,
+                           void* out, void* workspace, size_t workspace_bytes,
+                           si_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHADOWINFER_HIP_H */

@@ -1,0 +1,100 @@
+// Shared helpers for the gfx950 kernels of libshadowinfer_hip.so.
+//
+// Numerics policy: the library is compiled with -ffp-contract=off and
+// correctly rounded fp32 division, so every expression rounds exactly as
+// written; fused multiply-adds appear only where a kernel calls fmaf itself.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/shadowinfer_hip.h"
+
+namespace si {
+
+// ---- error reporting -------------------------------------------------------
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define SI_CHECK_ARG(cond, ...)             \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::si::set_error(__VA_ARGS__);         \
+      return SI_ERR_INVALID;                \
+    }                                       \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(si_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool dtype_ok(int dt) { return dt == SI_DT_F32 || dt == SI_DT_F16 || dt == SI_DT_BF16; }
+
+inline int dtype_size(int dt) { return dt == SI_DT_F32 ? 4 : 2; }
+
+// ---- scalar conversions (device) -------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Same rounding without the NaN test, for values known to be finite.
+__device__ __forceinline__ float round_bf16_finite(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__ushort_as_half((unsigned short)h);
+}
+
+// fp32 -> fp16 bits with the hardware conversion (round to nearest even).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__half_as_ushort(__float2half_rn(f));
+}
+
+// Element access by dtype code for the generic (shape-agnostic) kernels.
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == SI_DT_F32) return reinterpret_cast<const float*>(p)[i];
+  uint32_t h = reinterpret_cast<const uint16_t*>(p)[i];
+  return dt == SI_DT_F16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+}
+
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float v) {
+  if (dt == SI_DT_F32) {
+    reinterpret_cast<float*>(p)[i] = v;
+  } else {
+    uint32_t h = dt == SI_DT_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+    reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)h;
+  }
+}
+
+// Round an fp32 value to dtype dt and widen back (identity for fp32).
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == SI_DT_F32) return v;
+  if (dt == SI_DT_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  return bf16_bits_to_f32(f32_to_bf16_bits(v));
+}
+
+// |v| folded into a running maximum; NaN propagates like torch's max.
+__device__ __forceinline__ float amax_fold(float m, float v) {
+  float a = fabsf(v);
+  return (a != a || m != m) ? __uint_as_float(0x7fc00000u) : fmaxf(m, a);
+}
+
+}  // namespace si

@@ -1,0 +1,663 @@
+// Packed KV cache kernels for gfx950: pack, unpack, reuse copy, compaction.
+//
+// Row geometry. An entry e = t*H + h (token-major) owns, for each batch index
+// b, the input row K[b, h, t, :] of D values; in memory that is row
+// r = (b*H + h)*S + t of the [B*H*S, D] view. Inside a bucket the entry sits
+// at `slot` (from the plan scan), its batch rows at bucket row slot*B + b.
+// int4 entries keep the reference's per-entry byte row of ceil(B*D/2) bytes
+// holding the B*D nibbles in (b, d) order (packed_kv_cache.py:367-388).
+//
+// Fast pack path: LPR lanes of one wavefront share a row; each lane owns one
+// 16-byte chunk (8 bf16/fp16 or 4 fp32 values). Row and group maxima come from
+// butterfly shuffles inside the LPR lanes, so int8 (per row) and int4 (per
+// group) quantize with the same instruction stream; only the final stores
+// differ by precision. Reads walk K/V in memory order and are coalesced.
+#include "si_kv_common.h"
+
+namespace si {
+namespace {
+
+
+
+// ---------------------------------------------------------------------------
+// Quantization arithmetic shared by the fast and generic paths.
+// ---------------------------------------------------------------------------
+
+// Quotient round(T(x / s)) of Quantizer.quantize_int8/int4
+// (utils/quantization.py:141, 177) before clamping.
+//  - fp32/fp16 inputs: correctly rounded division, then rounding to T.
+//  - bf16 inputs with s >= 2^-100: x * r with r = RN(1/s), corrected by one
+//    fma on the exact remainder (Markstein's theorem: for r = RN(1/s) and a
+//    faithful q0, q0 + (x - q0*s)*r rounds to RN(x/s)). The identity with the
+//    correctly rounded path, after bf16 rounding and rint, has been checked
+//    exhaustively over every bf16 x and every bf16 s >= 2^-100 on the CPU.
+template <int DT>
+__device__ __forceinline__ float quant_quotient(float x, float s, float r, bool fast) {
+  float q;
+  if (DT == SI_DT_BF16) {
+    if (fast) {
+      const float q0 = x * r;
+      const float e = __builtin_fmaf(-q0, s, x);
+      q = __builtin_fmaf(e, r, q0);
+    } else {
+      q = x / s;
+    }
+    q = bf16_bits_to_f32(f32_to_bf16_bits(q));
+  } else if (DT == SI_DT_F16) {
+    q = f16_bits_to_f32(f32_to_f16_bits(x / s));
+  } else {
+    q = x / s;
+  }
+  return rintf(q);
+}
+
+// s = T(amax / div); s == 0 -> 1 (utils/quantization.py:138-140, 175-176).
+template <int DT>
+__device__ __forceinline__ float quant_scale(float amax, float div) {
+  float s = amax / div;
+  if (DT == SI_DT_BF16) s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+  if (DT == SI_DT_F16) s = f16_bits_to_f32(f32_to_f16_bits(s));
+  return s == 0.0f ? 1.0f : s;
+}
+
+template <int DT>
+__device__ __forceinline__ void store_scalar(void* p, int64_t i, float v) {
+  if (DT == SI_DT_F32) {
+    reinterpret_cast<float*>(p)[i] = v;
+  } else {
+    const uint32_t h = DT == SI_DT_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+    reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)h;
+  }
+}
+
+__device__ __forceinline__ float clampf(float v, float lo, float hi) {
+  return fminf(fmaxf(v, lo), hi);
+}
+
+// ---------------------------------------------------------------------------
+// 16-byte chunk loads: EPL values of dtype DT, widened to fp32.
+// ---------------------------------------------------------------------------
+
+template <int DT>
+struct Chunk {
+  static constexpr int EPL = DT == SI_DT_F32 ? 4 : 8;
+};
+
+template <int DT>
+__device__ __forceinline__ void load_chunk(const void* base, int64_t elem, float* out) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 raw = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) +
+                                     elem * (DT == SI_DT_F32 ? 4 : 2)));
+  const uint32_t w[4] = {raw[0], raw[1], raw[2], raw[3]};
+  if (DT == SI_DT_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (DT == SI_DT_BF16) {
+        out[2 * i] = __uint_as_float(w[i] << 16);
+        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        out[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+        out[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_f32(float* dst, const float* v) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4)
+    *reinterpret_cast<float4*>(dst + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+}
+
+template <int N>
+__device__ __forceinline__ void store_f16(uint16_t* dst, const float* v) {
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i)
+    w[i] = f32_to_f16_bits(v[2 * i]) | (f32_to_f16_bits(v[2 * i + 1]) << 16);
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  }
+}
+
+// Bytes of N int8 codes.
+template <int N>
+__device__ __forceinline__ void store_i8(int8_t* dst, const float* q) {
+  uint32_t w[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i)
+    w[i] = ((uint32_t)(int)q[4 * i] & 0xffu) | (((uint32_t)(int)q[4 * i + 1] & 0xffu) << 8) |
+           (((uint32_t)(int)q[4 * i + 2] & 0xffu) << 16) |
+           (((uint32_t)(int)q[4 * i + 3] & 0xffu) << 24);
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<uint32_t*>(dst) = w[0];
+  }
+}
+
+// N int4 codes -> N/2 bytes, high nibble first, nibble = code + 8.
+template <int N>
+__device__ __forceinline__ void store_i4(uint8_t* dst, const float* q) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const uint32_t hi = (uint32_t)((int)q[2 * i] + 8) & 0xfu;
+    const uint32_t lo = (uint32_t)((int)q[2 * i + 1] + 8) & 0xfu;
+    w |= ((hi << 4) | lo) << (8 * i);
+  }
+  if constexpr (N == 8) {
+    *reinterpret_cast<uint32_t*>(dst) = w;
+  } else {
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)w;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast pack: D = EPL * LPR, int4 group = EPL * lpg (lpg | LPR, power of two).
+// ---------------------------------------------------------------------------
+
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin,
+                                                    const void* __restrict__ vin, int64_t B,
+                                                    int64_t H, int64_t S, int lpg,
+                                                    const int8_t* __restrict__ code,
+                                                    const int32_t* __restrict__ slot,
+                                                    Buckets bk) {
+  constexpr int EPL = Chunk<DT>::EPL;
+  constexpr int D = EPL * LPR;
+  const int64_t rows = B * H * S;
+  const int lane = threadIdx.x % LPR;
+  const int groups = LPR / lpg;
+  const int64_t rb = B * D / 2;  // int4 bytes per entry (D even)
+  const int64_t step = (int64_t)gridDim.x * (blockDim.x / LPR);
+  for (int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR; row < rows;
+       row += step) {
+    const int64_t t = row % S;
+    const int64_t bh = row / S;
+    const int64_t h = bh % H;
+    const int64_t b = bh / H;
+    const int64_t e = t * H + h;
+    const int c = code[e];
+    if (c < 0 || c > 3) continue;
+    const int64_t s = slot[e];
+    float xk[EPL], xv[EPL];
+    load_chunk<DT>(kin, row * D + lane * EPL, xk);
+    load_chunk<DT>(vin, row * D + lane * EPL, xv);
+    const int64_t orow = s * B + b;
+    const int64_t oel = orow * D + lane * EPL;
+    if (c == SI_PREC_FP32) {
+      store_f32<EPL>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
+      store_f32<EPL>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
+      continue;
+    }
+    if (c == SI_PREC_FP16) {
+      store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
+      store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+      continue;
+    }
+    // int8 (per row) or int4 (per group): shared arithmetic.
+    float gk = 0.0f, gv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      gk = amax_fold(gk, xk[i]);
+      gv = amax_fold(gv, xv[i]);
+    }
+    for (int off = 1; off < lpg; off <<= 1) {
+      gk = amax_fold(gk, __shfl_xor(gk, off, 64));
+      gv = amax_fold(gv, __shfl_xor(gv, off, 64));
+    }
+    float mk = gk, mv = gv;
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) {
+      if (off >= lpg) {
+        mk = amax_fold(mk, __shfl_xor(mk, off, 64));
+        mv = amax_fold(mv, __shfl_xor(mv, off, 64));
+      }
+    }
+    const bool i8 = (c == SI_PREC_INT8);
+    const float sk = quant_scale<DT>(i8 ? mk : gk, i8 ? 127.0f : 7.0f);
+    const float sv = quant_scale<DT>(i8 ? mv : gv, i8 ? 127.0f : 7.0f);
+    const bool fk = sk >= 7.8886090522101181e-31f;  // 2^-100
+    const bool fv = sv >= 7.8886090522101181e-31f;
+    const float rk = 1.0f / sk;
+    const float rv = 1.0f / sv;
+    const float lo = i8 ? -128.0f : -8.0f;
+    const float hi = i8 ? 127.0f : 7.0f;
+    float qk[EPL], qv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      qk[i] = clampf(quant_quotient<DT>(xk[i], sk, rk, fk), lo, hi);
+      qv[i] = clampf(quant_quotient<DT>(xv[i], sv, rv, fv), lo, hi);
+    }
+    if (i8) {
+      store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[8]) + oel, qk);
+      store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[9]) + oel, qv);
+      if (lane == 0) {
+        store_scalar<DT>(bk.p[10], orow, sk);
+        store_scalar<DT>(bk.p[11], orow, sv);
+      }
+    } else {
+      const int64_t boff = s * rb + (b * D + lane * EPL) / 2;
+      store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[12]) + boff, qk);
+      store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[13]) + boff, qv);
+      if ((lane & (lpg - 1)) == 0) {
+        const int64_t si = orow * groups + lane / lpg;
+        store_scalar<DT>(bk.p[14], si, sk);
+        store_scalar<DT>(bk.p[15], si, sv);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic pack: one thread per entry, any B, D, group (odd sizes included).
+// ---------------------------------------------------------------------------
+
+template <int DT>
+__device__ void pack_entry_generic(const void* in, int64_t B, int64_t H, int64_t S, int64_t D,
+                                   int64_t g, int64_t t, int64_t h, int c, int64_t s,
+                                   void* data, void* scale) {
+  const int64_t L = B * D;
+  const int64_t rb = (L + 1) / 2;
+  const int64_t G = D / g;
+  uint32_t pending = 0;
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t src = ((b * H + h) * S + t) * D;
+    const int64_t orow = s * B + b;
+    if (c == SI_PREC_FP32 || c == SI_PREC_FP16) {
+      for (int64_t d = 0; d < D; ++d)
+        store_any(data, c == SI_PREC_FP32 ? SI_DT_F32 : SI_DT_F16, orow * D + d,
+                  load_any(in, DT, src + d));
+      continue;
+    }
+    const bool i8 = (c == SI_PREC_INT8);
+    const int64_t gs = i8 ? D : g;
+    for (int64_t g0 = 0; g0 < D; g0 += gs) {
+      float m = 0.0f;
+      for (int64_t d = 0; d < gs; ++d) m = amax_fold(m, load_any(in, DT, src + g0 + d));
+      const float sc = quant_scale<DT>(m, i8 ? 127.0f : 7.0f);
+      store_scalar<DT>(scale, i8 ? orow : orow * G + g0 / g, sc);
+      for (int64_t d = 0; d < gs; ++d) {
+        const float x = load_any(in, DT, src + g0 + d);
+        const float q = clampf(quant_quotient<DT>(x, sc, 0.0f, false), i8 ? -128.0f : -8.0f,
+                               i8 ? 127.0f : 7.0f);
+        if (i8) {
+          reinterpret_cast<int8_t*>(data)[orow * D + g0 + d] = (int8_t)(int)q;
+        } else {
+          const int64_t j = b * D + g0 + d;  // nibble index in the entry row
+          const uint32_t nib = (uint32_t)((int)q + 8) & 0xfu;
+          if ((j & 1) == 0) {
+            pending = nib << 4;
+          } else {
+            reinterpret_cast<uint8_t*>(data)[s * rb + j / 2] = (uint8_t)(pending | nib);
+          }
+        }
+      }
+    }
+  }
+  if (c == SI_PREC_INT4 && (L & 1)) reinterpret_cast<uint8_t*>(data)[s * rb + L / 2] =
+      (uint8_t)pending;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void kv_pack_generic(const void* __restrict__ kin,
+                                                       const void* __restrict__ vin, int64_t B,
+                                                       int64_t H, int64_t S, int64_t D,
+                                                       int64_t g, const int8_t* __restrict__ code,
+                                                       const int32_t* __restrict__ slot,
+                                                       Buckets bk) {
+  const int64_t n = S * H;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int c = code[e];
+    if (c < 0 || c > 3) continue;
+    const int64_t t = e / H;
+    const int64_t h = e - t * H;
+    const int64_t s = slot[e];
+    pack_entry_generic<DT>(kin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 0], bk.p[4 * c + 2]);
+    pack_entry_generic<DT>(vin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 1], bk.p[4 * c + 3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Unpack (packed_kv_cache.py:535-577): every output element is written.
+// ---------------------------------------------------------------------------
+
+// Dequantized value d of batch row b of the entry at `s` in bucket c.
+__device__ __forceinline__ float dequant_one(const Buckets& bk, int j, int c, int64_t s,
+                                             int64_t b, int64_t d, int64_t B, int64_t D,
+                                             int64_t g, int sdt) {
+  const int64_t orow = s * B + b;
+  if (c == SI_PREC_FP32) return reinterpret_cast<const float*>(bk.p[j])[orow * D + d];
+  if (c == SI_PREC_FP16)
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(bk.p[4 + j])[orow * D + d]);
+  if (c == SI_PREC_INT8)
+    return (float)reinterpret_cast<const int8_t*>(bk.p[8 + j])[orow * D + d] *
+           load_any(bk.p[10 + j], sdt, orow);
+  const int64_t rb = (B * D + 1) / 2;
+  const int64_t nib_idx = b * D + d;
+  const uint32_t byte = reinterpret_cast<const uint8_t*>(bk.p[12 + j])[s * rb + nib_idx / 2];
+  const int nib = (nib_idx & 1) ? (int)(byte & 0xfu) : (int)((byte >> 4) & 0xfu);
+  return (float)(nib - 8) * load_any(bk.p[14 + j], sdt, orow * (D / g) + d / g);
+}
+
+__global__ __launch_bounds__(256) void kv_unpack_generic(const int8_t* __restrict__ code,
+                                                         const int32_t* __restrict__ slot,
+                                                         Buckets bk, int sdt, int64_t B, int64_t H,
+                                                         int64_t S, int64_t D, int64_t g,
+                                                         float* __restrict__ ok,
+                                                         float* __restrict__ ov) {
+  const int64_t total = B * H * S * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = i % D;
+    const int64_t row = i / D;
+    const int64_t t = row % S;
+    const int64_t bh = row / S;
+    const int64_t h = bh % H;
+    const int64_t b = bh / H;
+    const int64_t e = t * H + h;
+    const int c = code[e];
+    float vk = 0.0f, vv = 0.0f;
+    if (c >= 0 && c <= 3) {
+      const int64_t s = slot[e];
+      vk = dequant_one(bk, 0, c, s, b, d, B, D, g, sdt);
+      vv = dequant_one(bk, 1, c, s, b, d, B, D, g, sdt);
+    }
+    ok[i] = vk;
+    ov[i] = vv;
+  }
+}
+
+template <int SDT>
+__global__ __launch_bounds__(256) void kv_unpack_vec4(const int8_t* __restrict__ code,
+                                                      const int32_t* __restrict__ slot, Buckets bk,
+                                                      int64_t B, int64_t H, int64_t S, int64_t D,
+                                                      int64_t g, float* __restrict__ ok,
+                                                      float* __restrict__ ov) {
+  const int64_t cpr = D / 4;
+  const int64_t total = B * H * S * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t ch = i % cpr;
+    const int64_t row = i / cpr;
+    const int64_t t = row % S;
+    const int64_t bh = row / S;
+    const int64_t h = bh % H;
+    const int64_t b = bh / H;
+    const int64_t e = t * H + h;
+    const int c = code[e];
+    float4 vk = make_float4(0.f, 0.f, 0.f, 0.f), vv = vk;
+    if (c >= 0 && c <= 3) {
+      const int64_t s = slot[e];
+      vk = dequant4<SDT>(bk, 0, c, s, b, ch * 4, B, D, g);
+      vv = dequant4<SDT>(bk, 1, c, s, b, ch * 4, B, D, g);
+    }
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(f32x4{vk.x, vk.y, vk.z, vk.w},
+                                reinterpret_cast<f32x4*>(ok + row * D + ch * 4));
+    __builtin_nontemporal_store(f32x4{vv.x, vv.y, vv.z, vv.w},
+                                reinterpret_cast<f32x4*>(ov + row * D + ch * 4));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row copies for reuse and compaction.
+// ---------------------------------------------------------------------------
+
+struct RowGeom {
+  int64_t data_bytes[4];   // per entry, per precision
+  int64_t scale_bytes[4];  // per entry, per precision (0 for fp32/fp16)
+};
+
+__host__ RowGeom make_geom(int64_t B, int64_t D, int64_t g, int sdt) {
+  RowGeom r;
+  const int64_t ssz = dtype_size(sdt);
+  r.data_bytes[0] = B * D * 4;
+  r.data_bytes[1] = B * D * 2;
+  r.data_bytes[2] = B * D;
+  r.data_bytes[3] = (B * D + 1) / 2;
+  r.scale_bytes[0] = 0;
+  r.scale_bytes[1] = 0;
+  r.scale_bytes[2] = B * ssz;
+  r.scale_bytes[3] = (g > 0 ? B * (D / g) : 0) * ssz;
+  return r;
+}
+
+// Copy n bytes with `lanes` cooperating lanes (lane index `lane`).
+__device__ __forceinline__ void copy_bytes(uint8_t* dst, const uint8_t* src, int64_t n, int lane,
+                                           int lanes) {
+  const uintptr_t mis = (reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) |
+                         (uintptr_t)n);
+  if ((mis & 15) == 0) {
+    for (int64_t i = lane; i < n / 16; i += lanes)
+      reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  } else if ((mis & 3) == 0) {
+    for (int64_t i = lane; i < n / 4; i += lanes)
+      reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+  } else {
+    for (int64_t i = lane; i < n; i += lanes) dst[i] = src[i];
+  }
+}
+
+__device__ __forceinline__ void copy_entry(const Buckets& dst, int64_t dslot, const Buckets& src,
+                                           int64_t sslot, int c, const RowGeom& geo, int lane,
+                                           int lanes) {
+  if (dst.p[4 * c] == nullptr) return;  // bucket not being rewritten
+  const int64_t db = geo.data_bytes[c];
+  const int64_t sb = geo.scale_bytes[c];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    copy_bytes(reinterpret_cast<uint8_t*>(dst.p[4 * c + j]) + dslot * db,
+               reinterpret_cast<const uint8_t*>(src.p[4 * c + j]) + sslot * db, db, lane, lanes);
+    if (sb)
+      copy_bytes(reinterpret_cast<uint8_t*>(dst.p[4 * c + 2 + j]) + dslot * sb,
+                 reinterpret_cast<const uint8_t*>(src.p[4 * c + 2 + j]) + sslot * sb, sb, lane,
+                 lanes);
+  }
+}
+
+constexpr int kCopyLanes = 16;
+
+__global__ __launch_bounds__(256) void kv_reuse_kernel(
+    const int8_t* __restrict__ cur_code, const int32_t* __restrict__ cur_slot, Buckets cur,
+    int64_t S, const int8_t* __restrict__ prev_code, const int32_t* __restrict__ prev_slot,
+    Buckets prev, int64_t S_prev, const uint8_t* __restrict__ mask, int64_t H, RowGeom geo,
+    unsigned long long* __restrict__ stats) {
+  const int lane = threadIdx.x % kCopyLanes;
+  const int64_t n = S * H;
+  unsigned long long applied = 0, skipped = 0;
+  const int64_t step = (int64_t)gridDim.x * (blockDim.x / kCopyLanes);
+  for (int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kCopyLanes; e < n;
+       e += step) {
+    const int c = cur_code[e];
+    if (c < 0 || c > 3 || mask[e] == 0) continue;
+    const int64_t t = e / H;
+    if (t >= S_prev) continue;  // (t, h) absent from the previous cache
+    const int pc = prev_code[e];  // same H, so the same token-major id
+    if (pc == c) {
+      copy_entry(cur, cur_slot[e], prev, prev_slot[e], c, geo, lane, kCopyLanes);
+      applied += (lane == 0);
+    } else if (pc >= 0 && pc <= 3) {
+      skipped += (lane == 0);
+    }
+  }
+  if (stats != nullptr) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      applied += __shfl_xor(applied, off, 64);
+      skipped += __shfl_xor(skipped, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0 && (applied | skipped)) {
+      atomicAdd(stats, applied);
+      atomicAdd(stats + 1, skipped);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_compact_kernel(
+    const int8_t* __restrict__ old_code, const int32_t* __restrict__ old_slot, Buckets oldb,
+    const int8_t* __restrict__ new_code, const int32_t* __restrict__ new_slot, Buckets newb,
+    int64_t n, RowGeom geo) {
+  const int lane = threadIdx.x % kCopyLanes;
+  const int64_t step = (int64_t)gridDim.x * (blockDim.x / kCopyLanes);
+  for (int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kCopyLanes; e < n;
+       e += step) {
+    const int c = new_code[e];
+    if (c < 0 || c > 3) continue;
+    copy_entry(newb, new_slot[e], oldb, old_slot[e], c, geo, lane, kCopyLanes);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+unsigned grid_for(int64_t work_items, int per_block, int64_t cap = 262144) {
+  int64_t blocks = ceil_div(work_items, per_block);
+  if (blocks < 1) blocks = 1;
+  if (blocks > cap) blocks = cap;
+  return (unsigned)blocks;
+}
+
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+template <int DT>
+int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, int64_t D,
+                int64_t g, const int8_t* code, const int32_t* slot, const Buckets& bk,
+                hipStream_t st) {
+  constexpr int EPL = Chunk<DT>::EPL;
+  const int64_t rows = B * H * S;
+  const int64_t lpr = D / EPL;
+  const int64_t lpg = g / EPL;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
+  const bool fast = aligned && D % EPL == 0 && pow2(lpr) && lpr <= 64 && lpr >= 1 &&
+                    g % EPL == 0 && pow2(lpg) && lpg <= lpr && (lpr == 8 || lpr == 16 ||
+                                                                 lpr == 32 || lpr == 64 ||
+                                                                 lpr == 4);
+  if (fast) {
+    const unsigned grid = grid_for(rows * lpr, 256);
+#define SI_PACK_CASE(L)                                                                      \
+  case L:                                                                                    \
+    kv_pack_fast<DT, L><<<grid, 256, 0, st>>>(k, v, B, H, S, (int)lpg, code, slot, bk);      \
+    break;
+    switch (lpr) {
+      SI_PACK_CASE(4)
+      SI_PACK_CASE(8)
+      SI_PACK_CASE(16)
+      SI_PACK_CASE(32)
+      SI_PACK_CASE(64)
+    }
+#undef SI_PACK_CASE
+    return check_launch("si_kv_pack/fast");
+  }
+  kv_pack_generic<DT><<<grid_for(S * H, 256), 256, 0, st>>>(k, v, B, H, S, D, g, code, slot, bk);
+  return check_launch("si_kv_pack/generic");
+}
+
+}  // namespace
+}  // namespace si
+
+using namespace si;
+
+extern "C" int si_kv_pack(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                          int64_t S, int64_t D, int64_t group, const int8_t* code,
+                          const int32_t* slot, void* const* buckets, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_kv_pack: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0, "si_kv_pack: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_pack: group %lld must divide D %lld",
+               (long long)group, (long long)D);
+  SI_CHECK_ARG(buckets != nullptr, "si_kv_pack: buckets table is NULL");
+  if (B * H * S == 0) return SI_OK;
+  SI_CHECK_ARG(k && v && code && slot, "si_kv_pack: NULL input");
+  const Buckets bk = to_buckets(buckets);
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case SI_DT_F32: return launch_pack<SI_DT_F32>(k, v, B, H, S, D, group, code, slot, bk, st);
+    case SI_DT_F16: return launch_pack<SI_DT_F16>(k, v, B, H, S, D, group, code, slot, bk, st);
+    default: return launch_pack<SI_DT_BF16>(k, v, B, H, S, D, group, code, slot, bk, st);
+  }
+}
+
+extern "C" int si_kv_unpack(const int8_t* code, const int32_t* slot, const void* const* buckets,
+                            int scale_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                            int64_t group, float* out_k, float* out_v, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_unpack: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0, "si_kv_unpack: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_unpack: group must divide D");
+  const int64_t total = B * H * S * D;
+  if (total == 0) return SI_OK;
+  SI_CHECK_ARG(code && slot && out_k && out_v && buckets, "si_kv_unpack: NULL argument");
+  const Buckets bk = to_buckets(buckets);
+  hipStream_t st = as_stream(stream);
+  const bool vec = D % 4 == 0 && group % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(out_k) | reinterpret_cast<uintptr_t>(out_v)) & 15) == 0;
+  if (vec) {
+    const unsigned grid = grid_for(total / 4, 256);
+    switch (scale_dtype) {
+      case SI_DT_F32:
+        kv_unpack_vec4<SI_DT_F32><<<grid, 256, 0, st>>>(code, slot, bk, B, H, S, D, group, out_k, out_v);
+        break;
+      case SI_DT_F16:
+        kv_unpack_vec4<SI_DT_F16><<<grid, 256, 0, st>>>(code, slot, bk, B, H, S, D, group, out_k, out_v);
+        break;
+      default:
+        kv_unpack_vec4<SI_DT_BF16><<<grid, 256, 0, st>>>(code, slot, bk, B, H, S, D, group, out_k, out_v);
+    }
+    return check_launch("si_kv_unpack/vec4");
+  }
+  kv_unpack_generic<<<grid_for(total, 256), 256, 0, st>>>(code, slot, bk, scale_dtype, B, H, S, D,
+                                                         group, out_k, out_v);
+  return check_launch("si_kv_unpack/generic");
+}
+
+extern "C" int si_kv_reuse(const int8_t* cur_code, const int32_t* cur_slot, void* const* cur_buckets,
+                           int64_t S, const int8_t* prev_code, const int32_t* prev_slot,
+                           const void* const* prev_buckets, int64_t S_prev, const uint8_t* mask,
+                           int64_t H, int64_t B, int64_t D, int64_t group, int scale_dtype,
+                           int64_t* stats, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_reuse: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(S >= 0 && S_prev >= 0 && H >= 0 && B >= 0 && D > 0, "si_kv_reuse: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_reuse: group must divide D");
+  const int64_t n = S * H;
+  if (n == 0) return SI_OK;
+  SI_CHECK_ARG(cur_code && cur_slot && mask && cur_buckets && prev_buckets,
+               "si_kv_reuse: NULL argument");
+  SI_CHECK_ARG(S_prev == 0 || (prev_code && prev_slot), "si_kv_reuse: NULL previous plan");
+  const RowGeom geo = make_geom(B, D, group, scale_dtype);
+  kv_reuse_kernel<<<grid_for(n * kCopyLanes, 256), 256, 0, as_stream(stream)>>>(
+      cur_code, cur_slot, to_buckets(cur_buckets), S, prev_code, prev_slot,
+      to_buckets(prev_buckets), S_prev, mask, H, geo,
+      reinterpret_cast<unsigned long long*>(stats));
+  return check_launch("si_kv_reuse");
+}
+
+extern "C" int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
+                             const void* const* old_buckets, const int8_t* new_code,
+                             const int32_t* new_slot, void* const* new_buckets, int64_t n,
+                             int64_t B, int64_t D, int64_t group, int scale_dtype,
+                             si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_compact: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(n >= 0 && B >= 0 && D > 0, "si_kv_compact: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_compact: group must divide D");
+  if (n == 0) return SI_OK;
+  SI_CHECK_ARG(old_code && old_slot && new_code && new_slot && old_buckets && new_buckets,
+               "si_kv_compact: NULL argument");
+  const RowGeom geo = make_geom(B, D, group, scale_dtype);
+  kv_compact_kernel<<<grid_for(n * kCopyLanes, 256), 256, 0, as_stream(stream)>>>(
+      old_code, old_slot, to_buckets(old_buckets), new_code, new_slot, to_buckets(new_buckets), n,
+      geo);
+  return check_launch("si_kv_compact");
+}

@@ -1,0 +1,46 @@
+"""Fused dequantize + bidirectional attention over a PackedKVCache.
+
+Replaces the reference's ``k, v = packed.unpack()`` followed by dense
+``softmax(q k^T / sqrt(D)) v`` without a mask
+(shadowinfer/models/simple_diffusion_llm.py:165-169) with one HIP kernel that
+dequantizes packed K/V tiles straight into LDS. Evicted token-heads behave as
+in the unpacked tensors: zero keys and values that still take part in the
+softmax.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _native
+from .packed_kv_cache import PackedKVCache
+
+
+def packed_attention(q: torch.Tensor, cache: PackedKVCache,
+                     sm_scale: Optional[float] = None) -> torch.Tensor:
+    """``q`` ``[B, H, S_q, D]`` (bf16 or fp16) against the cache's K/V
+    ``[B, H, S_kv, D]``; returns ``[B, H, S_q, D]`` in ``q.dtype``."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be [batch, heads, seq, dim], got {tuple(q.shape)}")
+    B, H, Sq, D = q.shape
+    if (B, H, D) != (cache.batch_size, cache.num_heads, cache.head_dim):
+        raise ValueError(
+            f"q shape {tuple(q.shape)} does not match the cache "
+            f"(batch={cache.batch_size}, heads={cache.num_heads}, head_dim={cache.head_dim})")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"q must be bfloat16 or float16, got {q.dtype}")
+    _native.require_device(q, "packed_attention")
+    code, slot, table, sdt, group = cache.device_state()
+    if code.device != q.device:
+        raise ValueError("q and the packed cache live on different devices")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qc = q.contiguous()
+    out = torch.empty_like(qc)
+    _native.call("si_attn_packed_fwd", qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
+                 code.data_ptr(), slot.data_ptr(), table, sdt, cache.seq_len, group,
+                 float(sm_scale), out.data_ptr(), _native.stream(q.device))
+    return out

@@ -1,0 +1,262 @@
+"""Precision/reuse plan with the reference API
+(shadowinfer/shadowkv/precision_plan.py:18-194).
+
+On a HIP device the grouping is computed by ``si_plan_scan``: every token-head
+gets its bucket position (slot) from prefix sums over the int8 ``[S, H]`` code
+matrix in token-major order, which is the order ``from_codes`` produces with
+``nonzero`` in the reference. ``flat_indices`` (``h*S + t`` per bucket) are
+scattered on the device too. The Python lists of the reference (``groups``,
+``evicted_entries``) and the SHA-256 ``fingerprint`` are materialized lazily,
+on first access, because the pack/unpack path never needs them.
+
+A plan whose ``device`` is the CPU holds the same metadata computed on the
+host, as the reference does for CPU tensors; such a plan cannot drive a device
+pack (``PackedKVCache.pack`` raises ValueError, as the reference does).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import struct
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+
+from .. import _native
+
+PRECISION_ORDER: Tuple[str, ...] = ("fp32", "fp16", "int8", "int4")
+EVICTED = "evicted"
+PRECISION_CODES: Dict[str, int] = {"fp32": 0, "fp16": 1, "int8": 2, "int4": 3, EVICTED: 4}
+CODE_PRECISIONS: Dict[int, str] = {code: name for name, code in PRECISION_CODES.items()}
+
+
+def map_to_codes(precision_map: Dict[int, Dict[int, str]], seq_len: int, num_heads: int,
+                 strict: bool = True, device: Any = "cpu") -> torch.Tensor:
+    """precision_plan.py:30-55: ``int8 [seq, heads]``; missing -> fp16; unknown
+    names raise ValueError when ``strict``, else become fp16."""
+    rows: List[List[int]] = []
+    for token_idx in range(seq_len):
+        token_map = precision_map.get(token_idx, {})
+        row: List[int] = []
+        for head_idx in range(num_heads):
+            raw = token_map.get(head_idx, "fp16")
+            precision = raw.lower() if isinstance(raw, str) else raw
+            if precision not in PRECISION_CODES:
+                if strict:
+                    raise ValueError(f"Unsupported precision: {raw}")
+                precision = "fp16"
+            row.append(PRECISION_CODES[precision])
+        rows.append(row)
+    return torch.tensor(rows, dtype=torch.int8, device=device).reshape(seq_len, num_heads)
+
+
+def codes_to_map(codes: torch.Tensor) -> Dict[int, Dict[int, str]]:
+    """precision_plan.py:58-69."""
+    values = codes.detach().to("cpu").to(torch.int64).tolist()
+    precision_map: Dict[int, Dict[int, str]] = {}
+    for token_idx, row in enumerate(values):
+        token_map: Dict[int, str] = {}
+        for head_idx, code in enumerate(row):
+            if code not in CODE_PRECISIONS:
+                raise ValueError(f"Unsupported precision code: {code}")
+            token_map[head_idx] = CODE_PRECISIONS[code]
+        precision_map[token_idx] = token_map
+    return precision_map
+
+
+class DeviceGrouping:
+    """Device-side result of the plan scan shared by plans and packed caches.
+
+    ``code``: int8 [S*H] sanitized codes (absent/unknown -> 4);
+    ``slot``: int32 [S*H] bucket positions (-1 if absent);
+    ``counts``: entries per code 0..4 (host ints).
+    """
+
+    __slots__ = ("code", "slot", "counts")
+
+    def __init__(self, code: torch.Tensor, slot: torch.Tensor, counts: List[int]):
+        self.code = code
+        self.slot = slot
+        self.counts = counts
+
+    @staticmethod
+    def scan(codes_flat: torch.Tensor, evict_mask: Optional[torch.Tensor] = None) -> "DeviceGrouping":
+        """Run si_plan_scan on int8 codes (token-major) on a HIP device."""
+        _native.require_device(codes_flat, "plan scan")
+        dev = codes_flat.device
+        n = codes_flat.numel()
+        ws_bytes = _native.size_query("si_plan_workspace_bytes", n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        code = torch.empty(n, dtype=torch.int8, device=dev)
+        slot = torch.empty(n, dtype=torch.int32, device=dev)
+        counts = torch.empty(5, dtype=torch.int64, device=dev)
+        _native.call("si_plan_scan", codes_flat.data_ptr(),
+                     _native.ptr(evict_mask), n, code.data_ptr(), slot.data_ptr(),
+                     counts.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream(dev))
+        return DeviceGrouping(code, slot, [int(c) for c in counts.tolist()])
+
+
+class PrecisionPlan:
+    """Immutable grouping/index plan shared by compress and pack
+    (precision_plan.py:72-84). Fields: seq_len, num_heads, codes, groups,
+    flat_indices, reuse_entries, reuse_flat, fingerprint, evicted_entries."""
+
+    __slots__ = ("seq_len", "num_heads", "codes", "flat_indices", "reuse_entries", "reuse_flat",
+                 "_groups", "_evicted", "_fingerprint", "_grouping", "_entries", "_frozen")
+
+    def __init__(self, seq_len: int, num_heads: int, codes: torch.Tensor,
+                 flat_indices: Dict[str, torch.Tensor], reuse_entries: List[Tuple[int, int]],
+                 reuse_flat: torch.Tensor, grouping: Optional[DeviceGrouping] = None,
+                 entries: Optional[Dict[str, torch.Tensor]] = None,
+                 groups: Optional[Dict[str, List[Tuple[int, int]]]] = None,
+                 evicted_entries: Optional[List[Tuple[int, int]]] = None,
+                 fingerprint: Optional[str] = None):
+        object.__setattr__(self, "_frozen", False)
+        self.seq_len = seq_len
+        self.num_heads = num_heads
+        self.codes = codes
+        self.flat_indices = flat_indices
+        self.reuse_entries = reuse_entries
+        self.reuse_flat = reuse_flat
+        self._grouping = grouping
+        self._entries = entries
+        self._groups = groups
+        self._evicted = evicted_entries
+        self._fingerprint = fingerprint
+        object.__setattr__(self, "_frozen", True)
+
+    def __setattr__(self, name, value):
+        if getattr(self, "_frozen", False) and not name.startswith("_"):
+            raise AttributeError(f"PrecisionPlan is immutable (cannot set {name!r})")
+        object.__setattr__(self, name, value)
+
+    # ------------------------------------------------------------------ build
+    @classmethod
+    def build(cls, precision_map: Dict[int, Dict[int, str]], seq_len: int, num_heads: int,
+              reuse_mask: Optional[Dict[Tuple[int, int], bool]] = None, device: Any = "cpu",
+              strict: bool = True) -> "PrecisionPlan":
+        """precision_plan.py:86-111."""
+        codes = map_to_codes(precision_map, seq_len, num_heads, strict=strict, device=device)
+        return cls.from_codes(codes, reuse_mask=reuse_mask, device=device)
+
+    @classmethod
+    def from_codes(cls, codes: torch.Tensor,
+                   reuse_mask: Optional[Dict[Tuple[int, int], bool]] = None,
+                   device: Any = None) -> "PrecisionPlan":
+        """precision_plan.py:113-177 (device grouping by prefix sums)."""
+        if codes.dim() != 2:
+            raise ValueError(f"codes must be 2-D [seq, heads], got shape {tuple(codes.shape)}")
+        seq_len, num_heads = int(codes.shape[0]), int(codes.shape[1])
+        if seq_len <= 0 or num_heads <= 0:
+            raise ValueError(f"seq_len and num_heads must be positive, got {seq_len}, {num_heads}")
+        if device is None:
+            device = codes.device
+        device = torch.device(device)
+        codes = codes.detach().to(device=device, dtype=torch.int8).contiguous()
+
+        reuse_entries: List[Tuple[int, int]] = []
+        if reuse_mask:
+            reuse_entries = sorted(
+                (int(t), int(h)) for (t, h), flag in reuse_mask.items()
+                if flag and 0 <= t < seq_len and 0 <= h < num_heads)
+        reuse_flat = torch.tensor([h * seq_len + t for t, h in reuse_entries], dtype=torch.long,
+                                  device=device)
+
+        if device.type == "cpu":
+            return cls._from_codes_host(codes, reuse_entries, reuse_flat)
+
+        grouping = DeviceGrouping.scan(codes.reshape(-1))
+        flat_indices: Dict[str, torch.Tensor] = {}
+        entries: Dict[str, torch.Tensor] = {}
+        for p, name in enumerate(PRECISION_ORDER):
+            flat_indices[name] = torch.empty(grouping.counts[p], dtype=torch.long, device=device)
+            entries[name] = torch.empty(grouping.counts[p], dtype=torch.int32, device=device)
+        _native.call("si_plan_scatter", grouping.code.data_ptr(), grouping.slot.data_ptr(),
+                     seq_len, num_heads,
+                     _native.table4([flat_indices[n].data_ptr() for n in PRECISION_ORDER]),
+                     _native.table4([entries[n].data_ptr() for n in PRECISION_ORDER]),
+                     _native.stream(device))
+        return cls(seq_len, num_heads, codes, flat_indices, reuse_entries, reuse_flat,
+                   grouping=grouping, entries=entries)
+
+    @classmethod
+    def _from_codes_host(cls, codes: torch.Tensor, reuse_entries, reuse_flat) -> "PrecisionPlan":
+        """Host metadata for a CPU plan (precision_plan.py:132-151)."""
+        seq_len, num_heads = int(codes.shape[0]), int(codes.shape[1])
+        flat = codes.reshape(-1).to(torch.int64)
+        groups: Dict[str, List[Tuple[int, int]]] = {p: [] for p in PRECISION_ORDER}
+        flat_indices: Dict[str, torch.Tensor] = {}
+        evicted: List[Tuple[int, int]] = []
+        for code, precision in CODE_PRECISIONS.items():
+            selected = (flat == code).nonzero(as_tuple=False).reshape(-1)
+            token_idx = torch.div(selected, num_heads, rounding_mode="floor")
+            head_idx = torch.remainder(selected, num_heads)
+            pairs = list(zip(token_idx.tolist(), head_idx.tolist()))
+            if precision == EVICTED:
+                evicted = pairs
+            else:
+                groups[precision] = pairs
+                flat_indices[precision] = (head_idx * seq_len + token_idx).to(torch.long)
+        return cls(seq_len, num_heads, codes, flat_indices, reuse_entries, reuse_flat,
+                   groups=groups, evicted_entries=evicted)
+
+    # ------------------------------------------------------------- lazy views
+    @property
+    def device(self) -> torch.device:
+        return self.codes.device
+
+    @property
+    def counts(self) -> List[int]:
+        """Entries per code 0..4."""
+        if self._grouping is not None:
+            return list(self._grouping.counts)
+        c = [len(self.groups[p]) for p in PRECISION_ORDER]
+        return c + [self.seq_len * self.num_heads - sum(c)]
+
+    @property
+    def groups(self) -> Dict[str, List[Tuple[int, int]]]:
+        if self._groups is None:
+            H = self.num_heads
+            groups: Dict[str, List[Tuple[int, int]]] = {}
+            for name in PRECISION_ORDER:
+                e = self._entries[name].to("cpu", torch.int64)
+                groups[name] = list(zip(torch.div(e, H, rounding_mode="floor").tolist(),
+                                        torch.remainder(e, H).tolist()))
+            object.__setattr__(self, "_groups", groups)
+        return self._groups
+
+    @property
+    def evicted_entries(self) -> List[Tuple[int, int]]:
+        if self._evicted is None:
+            sel = (self.codes.reshape(-1).to("cpu", torch.int64) == 4).nonzero().reshape(-1)
+            H = self.num_heads
+            object.__setattr__(self, "_evicted", list(zip(
+                torch.div(sel, H, rounding_mode="floor").tolist(),
+                torch.remainder(sel, H).tolist())))
+        return self._evicted
+
+    @property
+    def fingerprint(self) -> str:
+        """SHA-256 of ``<QQ`` (S, H) + code bytes + reuse_flat int64 bytes
+        (precision_plan.py:179-190)."""
+        if self._fingerprint is None:
+            digest = hashlib.sha256()
+            digest.update(struct.pack("<QQ", self.seq_len, self.num_heads))
+            digest.update(self.codes.detach().to("cpu").contiguous().numpy().tobytes())
+            digest.update(self.reuse_flat.detach().to("cpu").contiguous().numpy().tobytes())
+            object.__setattr__(self, "_fingerprint", digest.hexdigest())
+        return self._fingerprint
+
+    def reuse_set(self) -> set:
+        """precision_plan.py:192-194."""
+        return set(self.reuse_entries)
+
+    def device_grouping(self) -> DeviceGrouping:
+        """The device scan (code / slot / counts) driving a pack."""
+        if self._grouping is None:
+            raise ValueError("plan was built on the CPU; build it on the KV device")
+        return self._grouping
+
+    def __repr__(self) -> str:
+        return (f"PrecisionPlan(seq_len={self.seq_len}, num_heads={self.num_heads}, "
+                f"device={self.device}, counts={self.counts})")
