@@ -137,11 +137,13 @@ int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
  * (shadowinfer/models/simple_diffusion_llm.py:165-169) as one fused kernel
  * that dequantizes packed K/V tiles into LDS; the dense K/V never exist.
  * Semantic neighbour of shadowinfer/kernels/__init__.py:473-537.
- * q, out: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16; D = 64 or 128. */
+ * q: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16; D = 64 or 128.
+ * out: [B, H, S_q, D] in out_dtype (SI_DT_F32 matches unpack()'s fp32 K/V). */
 int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
                        int64_t D, const int8_t* code, const int32_t* slot,
                        const void* const* buckets, int scale_dtype, int64_t S_kv,
-                       int64_t group, float sm_scale, void* out, si_stream_t stream);
+                       int64_t group, float sm_scale, void* out, int out_dtype,
+                       si_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Quantizer                                                               */

@@ -38,10 +38,6 @@ __device__ __forceinline__ _Float16 q_to_h(uint32_t bits) {
   return (_Float16)f;
 }
 
-template <int QDT>
-__device__ __forceinline__ uint32_t out_bits(float v) {
-  return QDT == SI_DT_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
-}
 
 template <int D, int SDT, int QDT>
 __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restrict__ Q,
@@ -49,7 +45,7 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
                                                        int64_t Skv, const int8_t* __restrict__ code,
                                                        const int32_t* __restrict__ slot,
                                                        Buckets bk, int64_t g, float scale_log2,
-                                                       uint16_t* __restrict__ O) {
+                                                       void* __restrict__ O, int odt) {
   constexpr int KS = D / 16;   // MFMA k-steps over the head dim
   constexpr int DB = D / 32;   // 32-row blocks of O^T
   constexpr int DPT = D / 4;   // head-dim values per thread in the dequant stage
@@ -196,17 +192,25 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
 
   if (!m_ok) return;
   const float inv = 1.0f / l_run;
-  uint16_t* orow = O + ((b * H + h) * Sq + m) * D;
+  const int64_t obase = ((b * H + h) * Sq + m) * D;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = db * 32 + 8 * i + 4 * grp;
-      const uint32_t w0 = out_bits<QDT>(o[db][4 * i + 0] * inv) |
-                          (out_bits<QDT>(o[db][4 * i + 1] * inv) << 16);
-      const uint32_t w1 = out_bits<QDT>(o[db][4 * i + 2] * inv) |
-                          (out_bits<QDT>(o[db][4 * i + 3] * inv) << 16);
-      *reinterpret_cast<uint2*>(orow + d) = make_uint2(w0, w1);
+      const float r0 = o[db][4 * i + 0] * inv, r1 = o[db][4 * i + 1] * inv;
+      const float r2 = o[db][4 * i + 2] * inv, r3 = o[db][4 * i + 3] * inv;
+      if (odt == SI_DT_F32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(O) + obase + d) =
+            make_float4(r0, r1, r2, r3);
+      } else {
+        const bool bf = odt == SI_DT_BF16;
+        const uint32_t w0 = (bf ? f32_to_bf16_bits(r0) : f32_to_f16_bits(r0)) |
+                            ((bf ? f32_to_bf16_bits(r1) : f32_to_f16_bits(r1)) << 16);
+        const uint32_t w1 = (bf ? f32_to_bf16_bits(r2) : f32_to_f16_bits(r2)) |
+                            ((bf ? f32_to_bf16_bits(r3) : f32_to_f16_bits(r3)) << 16);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(O) + obase + d) = make_uint2(w0, w1);
+      }
     }
   }
 }
@@ -214,19 +218,19 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
 template <int D, int QDT>
 void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t B, int64_t H,
                  int64_t Sq, int64_t Skv, const int8_t* code, const int32_t* slot,
-                 const Buckets& bk, int64_t g, float scale_log2, uint16_t* out) {
+                 const Buckets& bk, int64_t g, float scale_log2, void* out, int odt) {
   switch (sdt) {
     case SI_DT_F32:
       attn_packed_fwd<D, SI_DT_F32, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk, g,
-                                                               scale_log2, out);
+                                                               scale_log2, out, odt);
       break;
     case SI_DT_F16:
       attn_packed_fwd<D, SI_DT_F16, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk, g,
-                                                               scale_log2, out);
+                                                               scale_log2, out, odt);
       break;
     default:
       attn_packed_fwd<D, SI_DT_BF16, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk,
-                                                                g, scale_log2, out);
+                                                                g, scale_log2, out, odt);
   }
 }
 
@@ -238,12 +242,14 @@ using namespace si;
 extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
                                   int64_t D, const int8_t* code, const int32_t* slot,
                                   const void* const* buckets, int scale_dtype, int64_t S_kv,
-                                  int64_t group, float sm_scale, void* out, si_stream_t stream) {
+                                  int64_t group, float sm_scale, void* out, int out_dtype,
+                                  si_stream_t stream) {
   clear_error();
   SI_CHECK_ARG(q_dtype == SI_DT_BF16 || q_dtype == SI_DT_F16,
                "si_attn_packed_fwd: q dtype must be bf16 or fp16 (got %d)", q_dtype);
   SI_CHECK_ARG(dtype_ok(scale_dtype), "si_attn_packed_fwd: unsupported scale dtype %d",
                scale_dtype);
+  SI_CHECK_ARG(dtype_ok(out_dtype), "si_attn_packed_fwd: unsupported out dtype %d", out_dtype);
   SI_CHECK_ARG(D == 64 || D == 128, "si_attn_packed_fwd: head_dim must be 64 or 128 (got %lld)",
                (long long)D);
   SI_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_kv > 0, "si_attn_packed_fwd: bad shape");
@@ -256,22 +262,21 @@ extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t
   const dim3 grid((unsigned)ceil_div(S_q, BM), (unsigned)H, (unsigned)B);
   const float scale_log2 = sm_scale * 1.4426950408889634f;
   const uint16_t* qp = reinterpret_cast<const uint16_t*>(q);
-  uint16_t* op = reinterpret_cast<uint16_t*>(out);
   hipStream_t st = as_stream(stream);
   if (D == 128) {
     if (q_dtype == SI_DT_BF16)
       launch_attn<128, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
-                                   group, scale_log2, op);
+                                   group, scale_log2, out, out_dtype);
     else
       launch_attn<128, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
-                                  group, scale_log2, op);
+                                  group, scale_log2, out, out_dtype);
   } else {
     if (q_dtype == SI_DT_BF16)
       launch_attn<64, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
-                                  group, scale_log2, op);
+                                  group, scale_log2, out, out_dtype);
     else
       launch_attn<64, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
-                                 group, scale_log2, op);
+                                 group, scale_log2, out, out_dtype);
   }
   return check_launch("si_attn_packed_fwd");
 }

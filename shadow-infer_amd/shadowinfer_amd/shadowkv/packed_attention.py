@@ -19,10 +19,11 @@ from .. import _native
 from .packed_kv_cache import PackedKVCache
 
 
-def packed_attention(q: torch.Tensor, cache: PackedKVCache,
-                     sm_scale: Optional[float] = None) -> torch.Tensor:
+def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[float] = None,
+                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """``q`` ``[B, H, S_q, D]`` (bf16 or fp16) against the cache's K/V
-    ``[B, H, S_kv, D]``; returns ``[B, H, S_q, D]`` in ``q.dtype``."""
+    ``[B, H, S_kv, D]``; returns ``[B, H, S_q, D]`` in ``out_dtype`` (fp32 by
+    default, the dtype of attention over the fp32 tensors unpack() returns)."""
     if q.dim() != 4:
         raise ValueError(f"q must be [batch, heads, seq, dim], got {tuple(q.shape)}")
     B, H, Sq, D = q.shape
@@ -39,8 +40,9 @@ def packed_attention(q: torch.Tensor, cache: PackedKVCache,
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     qc = q.contiguous()
-    out = torch.empty_like(qc)
+    out = torch.empty(qc.shape, dtype=out_dtype, device=qc.device)
     _native.call("si_attn_packed_fwd", qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
                  code.data_ptr(), slot.data_ptr(), table, sdt, cache.seq_len, group,
-                 float(sm_scale), out.data_ptr(), _native.stream(q.device))
+                 float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype),
+                 _native.stream(q.device))
     return out

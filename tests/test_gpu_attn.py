@@ -1,0 +1,115 @@
+"""GPU tests of the fused dequantize + bidirectional attention over a packed KV
+cache. Reference: unpack() -> softmax(q k^T / sqrt(D)) v with no mask, in
+double precision (the oracle at small sizes, a float64 torch computation on
+the device at the full sizes). Tolerance: relative L2 <= 1e-3.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import kv_inputs, mixed_codes, oracle_pack
+from oracle import oracle as O
+from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan, packed_attention
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _rel_l2(a, b):
+    a = torch.as_tensor(a).double()
+    b = torch.as_tensor(b).double()
+    return (torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b)).item()
+
+
+def _pack(k, v, codes, dev, group_size=16):
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    return PackedKVCache.pack(k.to(dev), v.to(dev), None, group_size=group_size,
+                              plan=plan)["packed_kv"]
+
+
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 128, 64, 128), (2, 2, 100, 200, 128),
+                                          (1, 3, 130, 257, 64), (1, 1, 1, 1, 64)])
+def test_attention_small_vs_oracle(dev, qdtype, B, H, Sq, Skv, D):
+    k, v = kv_inputs(B, H, Skv, D, torch.bfloat16, seed=Skv + D, outlier_frac=0.02)
+    codes = mixed_codes(Skv, H, seed=Skv, probs=(1, 1, 2, 1), sink=min(4, Skv), evicted=0.05)
+    cache = _pack(k, v, codes, dev)
+    g = torch.Generator().manual_seed(Sq)
+    q = torch.randn(B, H, Sq, D, generator=g).to(qdtype)
+    out = packed_attention(q.to(dev), cache)
+    assert out.dtype == torch.float32 and out.shape == (B, H, Sq, D)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
+    ref = O.attention(q.float().numpy().reshape(B * H, Sq, D), rk.reshape(B * H, Skv, D),
+                      rv.reshape(B * H, Skv, D)).reshape(B, H, Sq, D)
+    assert _rel_l2(out.float().cpu(), ref) <= TOL
+
+
+def _dense_reference(q, k, v):
+    """float64 softmax(q k^T / sqrt(D)) v on the device, one head at a time."""
+    B, H, Sq, D = q.shape
+    out = torch.empty(B, H, Sq, D, dtype=torch.float64, device=q.device)
+    for b in range(B):
+        for h in range(H):
+            qh = q[b, h].double()
+            kt = k[b, h].double().t().contiguous()
+            s = (qh @ kt) / math.sqrt(D)
+            p = torch.softmax(s, dim=-1)
+            out[b, h] = p @ v[b, h].double()
+    return out
+
+
+@pytest.mark.parametrize("S", [2048, 8192])
+def test_attention_config4(dev, S):
+    """B=1, 32 heads, head_dim 128, K/V bf16 with 1% outlier channels packed
+    with the 25/50/25 fp16/int8/int4 mixture and a 4-token sink; Q bf16."""
+    H, D = 32, 128
+    k, v = kv_inputs(1, H, S, D, torch.bfloat16, seed=S, outlier_frac=0.01)
+    codes = mixed_codes(S, H, seed=S, probs=(0, 0.25, 0.5, 0.25), sink=4)
+    cache = _pack(k, v, codes, dev)
+    g = torch.Generator().manual_seed(S + 1)
+    q = torch.randn(1, H, S, D, generator=g).to(torch.bfloat16).to(dev)
+    out = packed_attention(q, cache)
+    ku, vu = cache.unpack()
+    ref = _dense_reference(q, ku, vu)
+    err = (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item()
+    assert err <= TOL, err
+
+
+def test_attention_evicted_entries_take_part(dev):
+    """Evicted token-heads act as zero keys/values (score 0), as after unpack()."""
+    H, S, D = 2, 64, 64
+    k, v = kv_inputs(1, H, S, D, torch.bfloat16, seed=77)
+    codes = np.full((S, H), 2, np.int8)
+    codes[S // 2:] = 4
+    cache = _pack(k, v, codes, dev)
+    q = torch.randn(1, H, 16, D).to(torch.bfloat16)
+    out = packed_attention(q.to(dev), cache)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
+    ref = O.attention(q.float().numpy().reshape(H, 16, D), rk.reshape(H, S, D), rv.reshape(H, S, D))
+    assert _rel_l2(out.float().cpu().reshape(H, 16, D), ref) <= TOL
+
+
+def test_attention_low_precision_output(dev):
+    """bf16/fp16 outputs are the fp32 result rounded once (bf16 rounding alone
+    is ~1e-3 relative, so they are checked against the rounded fp32 output)."""
+    k, v = kv_inputs(1, 2, 96, 128, torch.bfloat16, seed=5)
+    cache = _pack(k, v, mixed_codes(96, 2, seed=5, probs=(1, 1, 1, 1)), dev)
+    q = torch.randn(1, 2, 64, 128).to(torch.bfloat16).to(dev)
+    ref = packed_attention(q, cache)
+    for dt in (torch.bfloat16, torch.float16):
+        out = packed_attention(q, cache, out_dtype=dt)
+        assert out.dtype == dt
+        assert torch.equal(out, ref.to(dt))
+
+
+def test_attention_errors(dev):
+    k, v = kv_inputs(1, 2, 16, 64, torch.bfloat16, seed=1)
+    cache = _pack(k, v, np.full((16, 2), 1, np.int8), dev)
+    with pytest.raises(ValueError):
+        packed_attention(torch.randn(1, 3, 8, 64, device=dev, dtype=torch.bfloat16), cache)
+    with pytest.raises(TypeError):
+        packed_attention(torch.randn(1, 2, 8, 64, device=dev), cache)

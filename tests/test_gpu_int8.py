@@ -1,0 +1,271 @@
+"""GPU parity tests for the INT8 FFN linear (int8_linear.py) and the Quantizer.
+
+Bar: quantized weights/activations, scales and int32 accumulators bit-exact
+with the oracle; the bf16/fp32 output of INT8Linear bit-exact too (the
+epilogue follows the reference's rounding order exactly).
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from helpers import DT, bits, to_np
+from oracle import oracle as O
+from shadowinfer_amd import _native
+from shadowinfer_amd.ffn_optimizer import INT8Linear, dequantized_weight, quantize_ffn_modules
+from shadowinfer_amd.kernels import _pack_int4, _unpack_int4
+from shadowinfer_amd.utils import Quantizer
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """si_gemm_i8i8_i32 through the C ABI."""
+    M, K = a.shape
+    N = b.shape[1]
+    c = torch.empty(M, N, dtype=torch.int32, device=a.device)
+    ws_bytes = _native.size_query("si_gemm_workspace_bytes", M, N, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=a.device)
+    _native.call("si_gemm_i8i8_i32", a.data_ptr(), b.data_ptr(), M, N, K, c.data_ptr(),
+                 ws.data_ptr(), ws_bytes, _native.stream(a.device))
+    return c
+
+
+def _act_quant(x: torch.Tensor):
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=torch.int8, device=x.device)
+    s = torch.empty(M, dtype=torch.float32, device=x.device)
+    _native.call("si_act_quant_i8", x.data_ptr(), _native.dtype_code(x.dtype), M, K, q.data_ptr(),
+                 s.data_ptr(), _native.stream(x.device))
+    return q, s
+
+
+def _exact_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Exact integer product on the device: float64 sums of int8 products stay
+    below 2^53, so the float64 GEMM is exact."""
+    return (a.double() @ b.double()).to(torch.int64)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 64, 16), (5, 128, 96), (16, 4096, 11008),
+                                   (64, 4096, 11008), (33, 256, 48), (300, 512, 272),
+                                   (7, 40, 24), (3, 17, 5)])
+def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
+    g = torch.Generator().manual_seed(M * 7 + K + N)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    b = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    c = _gemm_i32(a.to(dev), b.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(c, O.gemm_i8(a.numpy(), b.numpy()))
+
+
+@pytest.mark.parametrize("M", [256, 1024])
+def test_gemm_i32_large_m_exact(dev, M):
+    """Full FFN shape at large M against the exact float64 product."""
+    g = torch.Generator().manual_seed(M)
+    a = torch.randint(-127, 128, (M, 4096), generator=g, dtype=torch.int8).to(dev)
+    b = torch.randint(-127, 128, (4096, 11008), generator=g, dtype=torch.int8).to(dev)
+    c = _gemm_i32(a, b)
+    assert torch.equal(c.to(torch.int64), _exact_i32(a, b))
+
+
+def test_gemm_extreme_values_no_overflow(dev):
+    """All -127 x -127 over K=4096: the largest accumulator the layer can produce."""
+    a = torch.full((16, 4096), -127, dtype=torch.int8, device=dev)
+    b = torch.full((4096, 64), -127, dtype=torch.int8, device=dev)
+    assert torch.all(_gemm_i32(a, b) == 4096 * 127 * 127)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("M,K", [(16, 4096), (7, 128), (1024, 4096)])
+def test_act_quant_bit_exact(dev, dtype, M, K):
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    x[0] = 0  # zero row -> scale 1e-8
+    q, s = _act_quant(x.to(dev))
+    rq, rs = O.int8_act_quant(to_np(x), DT[dtype])
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+
+
+def test_weight_quant_bit_exact(dev):
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(11008, 4096, generator=g) * 0.02
+    w[5] = 0
+    lin = nn.Linear(4096, 11008, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+    q = INT8Linear.from_linear(lin.to(dev))
+    rq, rs = O.int8_weight_quant(w.numpy())
+    np.testing.assert_array_equal(q.qweight.cpu().numpy(), rq)
+    np.testing.assert_array_equal(q.weight_scale.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert q.qweight.shape == (4096, 11008) and q.qweight.dtype == torch.int8
+
+
+@pytest.fixture(scope="module")
+def ffn_layer(dev):
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn(11008, 4096, generator=g) * 0.02
+    lin = nn.Linear(4096, 11008, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+    return lin, INT8Linear.from_linear(lin.to(dev)), w
+
+
+@pytest.mark.parametrize("M", [16, 64, 256, 1024])
+def test_int8_linear_config2_bit_exact(dev, ffn_layer, M):
+    """X [M, 4096] bf16 ~ N(0,1), W [11008, 4096] ~ N(0, 0.02): quantized
+    activations and scales, int32 accumulators and the bf16 output bit-exact."""
+    _, layer, w = ffn_layer
+    g = torch.Generator().manual_seed(100 + M)
+    x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+    out = layer(x.to(dev))
+    assert out.dtype == torch.bfloat16 and out.shape == (M, 11008)
+    rq, rs = O.int8_act_quant(to_np(x), O.BF16)
+    qd, sd = _act_quant(x.to(dev))
+    np.testing.assert_array_equal(qd.cpu().numpy(), rq)
+    acc = _gemm_i32(qd, layer.qweight)
+    if M <= 64:
+        np.testing.assert_array_equal(acc.cpu().numpy(), O.gemm_i8(rq, layer.qweight.cpu().numpy()))
+    else:
+        assert torch.equal(acc.to(torch.int64), _exact_i32(qd, layer.qweight))
+    ref = O.int8_epilogue(acc.cpu().numpy(), rs, layer.weight_scale.cpu().numpy(), None, O.BF16)
+    np.testing.assert_array_equal(to_np(out), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_int8_linear_bias_bit_exact(dev, dtype):
+    torch.manual_seed(1)
+    lin = nn.Linear(128, 96, bias=True)
+    layer = INT8Linear.from_linear(lin.to(dev))
+    x = torch.randn(64, 128).to(dtype)
+    out = layer(x.to(dev))
+    ref, _, _, _ = O.int8_linear_forward(to_np(x), DT[dtype], layer.qweight.cpu().numpy(),
+                                         layer.weight_scale.cpu().numpy(),
+                                         layer.bias.cpu().numpy())
+    np.testing.assert_array_equal(to_np(out), ref)
+
+
+# --- reference test_int8_ffn.py behaviours, on the device ------------------
+def _rel_l2(a, b):
+    a, b = a.detach().float(), b.detach().float()
+    return (torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b).clamp_min(1e-12)).item()
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_relative_error_shape_dtype(dev, bias):
+    torch.manual_seed(0)
+    lin = nn.Linear(128, 96, bias=bias).to(dev)
+    layer = INT8Linear.from_linear(lin)
+    x = torch.randn(64, 128, device=dev)
+    out = layer(x)
+    assert out.shape == (64, 96) and out.dtype == x.dtype
+    assert _rel_l2(out, lin(x)) <= 0.03
+    assert layer.qweight.shape == (128, 96) and layer.weight_scale.dtype == torch.float32
+    assert (layer.bias is not None) == bias
+
+
+def test_batched_and_1d_inputs(dev):
+    torch.manual_seed(2)
+    layer = INT8Linear.from_linear(nn.Linear(128, 96, bias=True).to(dev))
+    x = torch.randn(2, 5, 128, device=dev)
+    batched = layer(x)
+    assert batched.shape == (2, 5, 96)
+    assert torch.equal(batched, layer(x.reshape(-1, 128)).reshape(2, 5, 96))
+    single = layer(x[0, 0])
+    assert single.shape == (96,) and torch.equal(single, batched[0, 0])
+
+
+@pytest.mark.parametrize("kind", ["zero", "constant", "large"])
+def test_extreme_inputs_finite(dev, kind):
+    torch.manual_seed(3)
+    layer = INT8Linear.from_linear(nn.Linear(128, 96, bias=True).to(dev))
+    x = {"zero": torch.zeros(4, 128), "constant": torch.full((4, 128), 0.5),
+         "large": torch.randn(4, 128) * 1e4}[kind].to(dev)
+    out = layer(x)
+    assert bool(torch.isfinite(out).all())
+
+
+def test_empty_invalid_and_memory(dev):
+    layer = INT8Linear.from_linear(nn.Linear(128, 96, bias=True).to(dev))
+    assert layer(torch.empty(0, 128, device=dev)).shape == (0, 96)
+    with pytest.raises(ValueError):
+        layer(torch.randn(4, 127, device=dev))
+    assert layer.memory_bytes() == 128 * 96 + 4 * 96 + 4 * 96
+    assert layer.dense_equivalent_bytes() == 4 * 128 * 96 + 4 * 96
+    assert layer.using_int_mm
+    dq = dequantized_weight(layer)
+    assert dq.shape == (128, 96)
+
+
+def test_quantize_ffn_modules(dev):
+    class MLP(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.up_proj = nn.Linear(64, 128)
+            self.down_proj = nn.Linear(128, 64)
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.mlp = MLP()
+            self.other = nn.Linear(64, 64)
+
+    model = Block().to(dev)
+    stats = quantize_ffn_modules(model, keep_fp32_reference=True)
+    assert stats["supported"] and stats["modules"] == 2 and not stats["fallback"]
+    assert isinstance(model.mlp.up_proj, INT8Linear) and isinstance(model.other, nn.Linear)
+    again = quantize_ffn_modules(model)
+    assert again["modules"] == 2
+    assert quantize_ffn_modules(nn.Linear(4, 4).to(dev)) == {"supported": False}
+
+
+# --- Quantizer on the device ----------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_quantizer_int8_int4_bit_exact(dev, dtype):
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(10, 3, 64, generator=g).to(dtype)
+    q, s = Quantizer.quantize_int8(x.to(dev))
+    rq, rs = O.quant_rows_i8(to_np(x), DT[dtype])
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    np.testing.assert_array_equal(bits(s), rs.reshape(-1).view(np.uint8))
+    q4, s4 = Quantizer.quantize_int4(x.to(dev), group_size=16)
+    rq4, rs4 = O.quant_rows_i4(to_np(x), DT[dtype], 16)
+    assert q4.shape == (10, 3, 4, 16) and s4.shape == (10, 3, 4, 1)
+    np.testing.assert_array_equal(q4.cpu().numpy(), rq4)
+    np.testing.assert_array_equal(bits(s4), rs4.reshape(-1).view(np.uint8))
+    dq = Quantizer.dequantize_int8(q, s)
+    np.testing.assert_array_equal(dq.cpu().numpy(), O.dequant_rows(rq, rs, DT[dtype], 64))
+    dq4 = Quantizer.dequantize_int4(q4, s4)
+    assert dq4.shape == (10, 3, 64)
+    with pytest.raises(ValueError):
+        Quantizer.quantize_int4(x.to(dev), group_size=24)
+
+
+def test_quantizer_known_answers(dev):
+    """Scale of [1, -2, 3, -4] is 4/127 (reference test_kernels.py:72-77);
+    zero rows get scale 1 and codes 0."""
+    q, s = Quantizer.quantize_int8(torch.tensor([[1.0, -2.0, 3.0, -4.0]], device=dev))
+    assert abs(s.item() - 4.0 / 127.0) < 1e-6
+    assert q.tolist() == [[32, -64, 95, -127]]
+    q0, s0 = Quantizer.quantize_int8(torch.zeros(2, 8, device=dev))
+    assert torch.all(s0 == 1) and torch.all(q0 == 0)
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 23, 128, 1001])
+def test_int4_pack_unpack(dev, n):
+    g = torch.Generator().manual_seed(n)
+    t = torch.randint(-8, 8, (n,), generator=g, dtype=torch.int8)
+    packed = Quantizer.pack_int4(t.to(dev))
+    assert packed.dtype == torch.uint8 and packed.numel() == (n + 1) // 2
+    np.testing.assert_array_equal(packed.cpu().numpy(), O.pack_int4_flat(t.numpy()))
+    assert torch.equal(Quantizer.unpack_int4(packed, n).cpu(), t)
+    assert torch.equal(_unpack_int4(_pack_int4(t.to(dev)), n).cpu(), t)
+
+
+def test_int4_all_nibble_pairs(dev):
+    """Every (hi, lo) pair of codes in [-8, 7] packs to ((hi+8) << 4) | (lo+8)."""
+    hi, lo = torch.meshgrid(torch.arange(-8, 8), torch.arange(-8, 8), indexing="ij")
+    t = torch.stack([hi.reshape(-1), lo.reshape(-1)], dim=1).reshape(-1).to(torch.int8)
+    packed = Quantizer.pack_int4(t.to(dev)).cpu()
+    expected = ((hi.reshape(-1) + 8) << 4) | (lo.reshape(-1) + 8)
+    assert torch.equal(packed.to(torch.int64), expected)
