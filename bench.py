@@ -1,0 +1,377 @@
+"""Benchmark of the quantized data plane on one MI355X.
+
+Headline (``value``): KV pack+unpack throughput in GB/s over the 7B-shaped
+cache - 32 layers x B=1 x S=8192 x H=32 x D=128, bf16 K/V ~ N(0,1) with 1%
+outlier channels x8, precision codes 25% fp16 / 50% int8 / 25% int4 (group
+16) with a 4-token fp16 sink. One step = for every layer, pack (dense K/V ->
+precision buckets) then unpack (buckets -> fp32 K/V); inputs, plans and
+buckets are resident in HBM before the timed region. Throughput counts the
+algorithmic bytes: pack reads K+V and the code matrix and writes the packed
+bytes; unpack reads the packed bytes and the codes and writes fp32 K+V
+(slot metadata excluded).
+
+Also reported on the same JSON line: per-kernel times with the roofline of the
+dominant kernel, the INT8 FFN GEMM (4096 x 11008, M in {16, 64, 256, 1024}) in
+TOPS against the int8 MFMA peak, the fused packed-KV attention, and the CPU
+baseline (the oracle on the host, a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "shadow-infer_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, TOPS
+FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16/bf16 MFMA, TFLOP/s
+
+LAYERS, B, S, H, D = 32, 1, 8192, 32, 128
+GROUP = 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_codes(seed: int):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    codes = rng.choice(np.array([1, 2, 3], np.int8), size=(S, H), p=[0.25, 0.5, 0.25])
+    codes[:4, :] = 1
+    return codes
+
+
+def make_kv(gen, device, dtype):
+    import torch
+    k = torch.randn(B, H, S, D, generator=gen, device=device)
+    v = torch.randn(B, H, S, D, generator=gen, device=device)
+    ch = torch.randperm(D, generator=gen, device=device)[: max(1, round(0.01 * D))]
+    k[..., ch] *= 8
+    v[..., ch] *= 8
+    return k.to(dtype), v.to(dtype)
+
+
+class EventTimer:
+    """HIP events recorded on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def time(self, fn, reps: int) -> float:
+        torch = self.torch
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(self.stream)
+        for _ in range(reps):
+            fn()
+        end.record(self.stream)
+        end.synchronize()
+        return start.elapsed_time(end) / reps  # ms
+
+
+def bench_kv(torch, dev, steps, warmup):
+    from shadowinfer_amd import _native
+    from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan
+
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    layers = []
+    for layer in range(LAYERS):
+        k, v = make_kv(gen, dev, torch.bfloat16)
+        codes = make_codes(1000 + layer)
+        plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+        cache = PackedKVCache.pack(k, v, None, group_size=GROUP, plan=plan)["packed_kv"]
+        code, slot, table, sdt, group = cache.device_state()
+        ok = torch.empty(B, H, S, D, dtype=torch.float32, device=dev)
+        ov = torch.empty_like(ok)
+        layers.append(dict(k=k, v=v, code=code, slot=slot, table=table, sdt=sdt, cache=cache,
+                           ok=ok, ov=ov, packed=cache.memory_bytes()))
+    torch.cuda.synchronize()
+
+    def pack(L):
+        _native.call("si_kv_pack", L["k"].data_ptr(), L["v"].data_ptr(), _native.DT_BF16, B, H, S,
+                     D, GROUP, L["code"].data_ptr(), L["slot"].data_ptr(), L["table"], sptr)
+
+    def unpack(L):
+        _native.call("si_kv_unpack", L["code"].data_ptr(), L["slot"].data_ptr(), L["table"],
+                     L["sdt"], B, H, S, D, GROUP, L["ok"].data_ptr(), L["ov"].data_ptr(), sptr)
+
+    def step():
+        for L in layers:
+            pack(L)
+            unpack(L)
+
+    dense_in = 2 * B * H * S * D * 2          # K + V bf16
+    codes_b = S * H                            # int8 codes
+    fp32_out = 2 * B * H * S * D * 4           # K + V fp32
+    pack_bytes = [dense_in + codes_b + L["packed"] for L in layers]
+    unpack_bytes = [L["packed"] + codes_b + fp32_out for L in layers]
+    step_bytes = sum(pack_bytes) + sum(unpack_bytes)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch, stream)
+    t0 = time.perf_counter()
+    ms_step = timer.time(step, steps)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+
+    # Per-kernel averages: each launch on its own layer (distinct buffers).
+    reps = max(2, steps // 4)
+    ms_pack = timer.time(lambda: [pack(L) for L in layers], reps) / LAYERS
+    ms_unpack = timer.time(lambda: [unpack(L) for L in layers], reps) / LAYERS
+    avg_pack_b = sum(pack_bytes) / LAYERS
+    avg_unpack_b = sum(unpack_bytes) / LAYERS
+    res = {
+        "ms_per_step": ms_step,
+        "wall_ms_per_step": wall,
+        "step_bytes": step_bytes,
+        "gbs": step_bytes / (ms_step * 1e-3) / 1e9,
+        "pack_us": ms_pack * 1e3,
+        "unpack_us": ms_unpack * 1e3,
+        "pack_gbs": avg_pack_b / (ms_pack * 1e-3) / 1e9,
+        "unpack_gbs": avg_unpack_b / (ms_unpack * 1e-3) / 1e9,
+        "pack_bytes_per_launch": avg_pack_b,
+        "unpack_bytes_per_launch": avg_unpack_b,
+        "packed_bytes_per_layer": sum(L["packed"] for L in layers) / LAYERS,
+    }
+
+    # The reference-API path (plan given, buckets allocated per call, unpack
+    # allocating its outputs), for context: one layer, wall clock.
+    L0 = layers[0]
+    plan0 = PrecisionPlan.from_codes(torch.from_numpy(make_codes(1000)).to(dev))
+
+    def api_roundtrip():
+        c = PackedKVCache.pack(L0["k"], L0["v"], None, group_size=GROUP, plan=plan0)["packed_kv"]
+        c.unpack()
+
+    for _ in range(3):
+        api_roundtrip()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        api_roundtrip()
+    torch.cuda.synchronize()
+    res["api_layer_ms"] = (time.perf_counter() - t0) / 10 * 1e3
+
+    # Plan build (from_codes on the device, including the host copy of the counts).
+    codes_dev = torch.from_numpy(make_codes(1000)).to(dev)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        PrecisionPlan.from_codes(codes_dev)
+    torch.cuda.synchronize()
+    res["plan_from_codes_ms"] = (time.perf_counter() - t0) / 10 * 1e3
+
+    # Reuse (50% mask) and evict (25%) on one layer, for context.
+    prev = layers[1]["cache"]
+    cur = layers[0]["cache"]
+    mask = (torch.rand(S, H, generator=gen, device=dev) < 0.5)
+    ms_reuse = timer.time(lambda: cur.apply_reuse_mask(prev, mask), 5)
+    res["reuse50_us"] = ms_reuse * 1e3
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_gemm(torch, dev, iters=50):
+    from shadowinfer_amd import _native
+
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+    K, N = 4096, 11008
+    gen = torch.Generator(device=dev).manual_seed(7)
+    copies = 8  # 8 x 45 MB of weights: more than the 256 MB last-level cache
+    ws = [torch.randint(-127, 128, (K, N), generator=gen, device=dev, dtype=torch.int8)
+          for _ in range(copies)]
+    sw = torch.rand(N, generator=gen, device=dev) * 1e-3 + 1e-4
+    timer = EventTimer(torch, stream)
+    out = {}
+    for M in (16, 64, 256, 1024):
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        q = torch.empty(M, K, dtype=torch.int8, device=dev)
+        sx = torch.empty(M, dtype=torch.float32, device=dev)
+        c = torch.empty(M, N, dtype=torch.int32, device=dev)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        gws_b = _native.size_query("si_gemm_workspace_bytes", M, N, K)
+        gws = torch.empty(max(gws_b, 1), dtype=torch.uint8, device=dev)
+        lws_b = _native.size_query("si_int8_linear_workspace_bytes", M, K, N)
+        lws = torch.empty(lws_b, dtype=torch.uint8, device=dev)
+        _native.call("si_act_quant_i8", x.data_ptr(), _native.DT_BF16, M, K, q.data_ptr(),
+                     sx.data_ptr(), sptr)
+        it = [0]
+
+        def gemm():
+            w = ws[it[0] % copies]
+            it[0] += 1
+            _native.call("si_gemm_i8i8_i32", q.data_ptr(), w.data_ptr(), M, N, K, c.data_ptr(),
+                         gws.data_ptr(), gws_b, sptr)
+
+        def forward():
+            w = ws[it[0] % copies]
+            it[0] += 1
+            _native.call("si_int8_linear_forward", x.data_ptr(), _native.DT_BF16, M, K, N,
+                         w.data_ptr(), sw.data_ptr(), None, y.data_ptr(), lws.data_ptr(), lws_b,
+                         sptr)
+
+        for _ in range(5):
+            gemm()
+            forward()
+        ms_gemm = timer.time(gemm, iters)
+        ms_fwd = timer.time(forward, iters)
+        ops = 2.0 * M * K * N
+        out[str(M)] = {
+            "gemm_us": ms_gemm * 1e3,
+            "gemm_tops": ops / (ms_gemm * 1e-3) / 1e12,
+            "gemm_frac": ops / (ms_gemm * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+            "gemm_weight_gbs": K * N / (ms_gemm * 1e-3) / 1e9,
+            "forward_us": ms_fwd * 1e3,
+            "forward_tops": ops / (ms_fwd * 1e-3) / 1e12,
+        }
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_attention(torch, dev, iters=10):
+    from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan, packed_attention
+
+    res = {}
+    gen = torch.Generator(device=dev).manual_seed(11)
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    for Sq in (2048, 8192):
+        k = torch.randn(1, H, Sq, D, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, H, Sq, D, generator=gen, device=dev).to(torch.bfloat16)
+        codes = torch.from_numpy(make_codes(5)[:Sq]).to(dev) if Sq <= S else None
+        plan = PrecisionPlan.from_codes(codes)
+        cache = PackedKVCache.pack(k, v, None, group_size=GROUP, plan=plan)["packed_kv"]
+        q = torch.randn(1, H, Sq, D, generator=gen, device=dev).to(torch.bfloat16)
+        for _ in range(2):
+            packed_attention(q, cache)
+        ms = timer.time(lambda: packed_attention(q, cache), iters)
+        flops = 4.0 * H * Sq * Sq * D
+        res[str(Sq)] = {"us": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
+                        "frac": flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS}
+    return res
+
+
+def cpu_baseline(layers: int = 4):
+    """The oracle (C + numpy, one thread) on ``layers`` of the same layers:
+    pack + unpack, algorithmic bytes / wall time."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+
+    O.build()
+    total_bytes, total_s = 0, 0.0
+    gen = torch.Generator().manual_seed(99)
+    for layer in range(layers):
+        k = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
+        v = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
+        kn = k.view(torch.int16).numpy().view(np.uint16)
+        vn = v.view(torch.int16).numpy().view(np.uint16)
+        codes = make_codes(1000 + layer)
+        t0 = time.perf_counter()
+        cache = O.kv_pack(kn, vn, O.BF16, codes, GROUP)
+        O.kv_unpack(cache)
+        total_s += time.perf_counter() - t0
+        packed = cache.memory_bytes()
+        total_bytes += (2 * B * H * S * D * 2 + S * H + packed) + (packed + S * H + 2 * B * H * S * D * 4)
+    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{layers} of the 32 layers (pack+unpack), oracle in C + numpy, 1 thread",
+            "seconds": total_s}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="skip GEMM and attention extras")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    log(f"device {torch.cuda.get_device_name(dev)}")
+
+    log("kv pack+unpack")
+    kv = bench_kv(torch, dev, args.steps, args.warmup)
+    log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
+    gemm = attn = None
+    if not args.quick:
+        log("int8 gemm")
+        gemm = bench_gemm(torch, dev)
+        log("attention")
+        attn = bench_attention(torch, dev)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        cpu = cpu_baseline()
+        log(f"cpu {cpu['value']:.3f} GB/s in {cpu['seconds']:.1f} s")
+
+    dom = "unpack" if kv["unpack_us"] >= kv["pack_us"] else "pack"
+    achieved = kv[f"{dom}_gbs"]
+    line = {
+        "metric": "KV pack+unpack GB/s (%HBM peak); INT8 FFN GEMM TOPS (%MFMA peak)",
+        "value": round(kv["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(kv["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "PackedKVCache pack+unpack, 32 layers x B=1 x S=8192 x H=32 x D=128, "
+                        "bf16 K/V, codes 25% fp16 / 50% int8 / 25% int4 g16, 4-token fp16 sink",
+            "layers": LAYERS, "batch": B, "seq_len": S, "heads": H, "head_dim": D,
+            "int4_group": GROUP, "hbm_frac": round(kv["gbs"] / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "kernel": f"kv_{dom}",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(kv[f"{dom}_bytes_per_launch"]),
+            "avg_launch_us": round(kv[f"{dom}_us"], 3),
+        },
+        "cpu_baseline": cpu and {k: (round(v, 4) if isinstance(v, float) else v)
+                                 for k, v in cpu.items() if k != "seconds"},
+        "kv": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in kv.items()},
+    }
+    if gemm is not None:
+        line["int8_gemm"] = {"shape": "M x 4096 x 11008", "peak_tops": INT8_PEAK_TOPS,
+                             **{m: {k: round(v, 4) for k, v in r.items()} for m, r in gemm.items()}}
+    if attn is not None:
+        line["packed_attention"] = {"shape": "B=1, H=32, D=128, S_q=S_kv", "peak_tflops": FP16_PEAK_TFLOPS,
+                                    **{s: {k: round(v, 4) for k, v in r.items()} for s, r in attn.items()}}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
