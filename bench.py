@@ -126,10 +126,21 @@ def bench_kv(torch, dev, steps, warmup):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
 
-    # Per-kernel averages: each launch on its own layer (distinct buffers).
+    # Per-launch durations inside the same step loop: an event pair around
+    # every pack and every unpack launch, on the launch stream.
     reps = max(2, steps // 4)
-    ms_pack = timer.time(lambda: [pack(L) for L in layers], reps) / LAYERS
-    ms_unpack = timer.time(lambda: [unpack(L) for L in layers], reps) / LAYERS
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(LAYERS * reps)]
+    for r in range(reps):
+        for i, L in enumerate(layers):
+            e0, e1, e2 = evs[r * LAYERS + i]
+            e0.record(stream)
+            pack(L)
+            e1.record(stream)
+            unpack(L)
+            e2.record(stream)
+    torch.cuda.synchronize()
+    ms_pack = sum(e0.elapsed_time(e1) for e0, e1, _ in evs) / len(evs)
+    ms_unpack = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / len(evs)
     avg_pack_b = sum(pack_bytes) / LAYERS
     avg_unpack_b = sum(unpack_bytes) / LAYERS
     res = {
@@ -300,6 +311,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="skip GEMM and attention extras")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run a plain 512 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -313,6 +326,14 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(dev)}")
 
+    if args.calib:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 3 x 512 MiB device-to-device")
+        del src, dst
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
     log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")

@@ -162,97 +162,316 @@ __device__ __forceinline__ void store_i4(uint8_t* dst, const float* q) {
 
 // ---------------------------------------------------------------------------
 // Fast pack: D = EPL * LPR, int4 group = EPL * lpg (lpg | LPR, power of two).
+// Grid: blockIdx.y = b*H + h, blockIdx.x = tile of RPP*U tokens; each thread
+// keeps U rows in flight (loads issued before any row is quantized).
 // ---------------------------------------------------------------------------
 
 template <int DT, int LPR>
+__device__ __forceinline__ void pack_row(const float* xk, const float* xv, int c, int s, int b,
+                                         int B, int lane, int lpg, const Buckets& bk) {
+  constexpr int EPL = Chunk<DT>::EPL;
+  constexpr int D = EPL * LPR;
+  const int64_t orow = (int64_t)s * B + b;
+  const int64_t oel = orow * D + lane * EPL;
+  if (c == SI_PREC_FP32) {
+    store_f32<EPL>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
+    store_f32<EPL>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
+    return;
+  }
+  if (c == SI_PREC_FP16) {
+    store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
+    store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+    return;
+  }
+  // int8 (per row) or int4 (per group): shared arithmetic.
+  float gk = 0.0f, gv = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    gk = amax_fold(gk, xk[i]);
+    gv = amax_fold(gv, xv[i]);
+  }
+  for (int off = 1; off < lpg; off <<= 1) {
+    gk = amax_fold(gk, __shfl_xor(gk, off, 64));
+    gv = amax_fold(gv, __shfl_xor(gv, off, 64));
+  }
+  float mk = gk, mv = gv;
+#pragma unroll
+  for (int off = 1; off < LPR; off <<= 1) {
+    if (off >= lpg) {
+      mk = amax_fold(mk, __shfl_xor(mk, off, 64));
+      mv = amax_fold(mv, __shfl_xor(mv, off, 64));
+    }
+  }
+  const bool i8 = (c == SI_PREC_INT8);
+  const float sk = quant_scale<DT>(i8 ? mk : gk, i8 ? 127.0f : 7.0f);
+  const float sv = quant_scale<DT>(i8 ? mv : gv, i8 ? 127.0f : 7.0f);
+  const bool fk = sk >= 7.8886090522101181e-31f;  // 2^-100
+  const bool fv = sv >= 7.8886090522101181e-31f;
+  const float rk = 1.0f / sk;
+  const float rv = 1.0f / sv;
+  const float lo = i8 ? -128.0f : -8.0f;
+  const float hi = i8 ? 127.0f : 7.0f;
+  float qk[EPL], qv[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    qk[i] = clampf(quant_quotient<DT>(xk[i], sk, rk, fk), lo, hi);
+    qv[i] = clampf(quant_quotient<DT>(xv[i], sv, rv, fv), lo, hi);
+  }
+  if (i8) {
+    store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[8]) + oel, qk);
+    store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[9]) + oel, qv);
+    if (lane == 0) {
+      store_scalar<DT>(bk.p[10], orow, sk);
+      store_scalar<DT>(bk.p[11], orow, sv);
+    }
+  } else {
+    const int64_t rb = (int64_t)B * D / 2;  // int4 bytes per entry (D even)
+    const int64_t boff = (int64_t)s * rb + ((int64_t)b * D + lane * EPL) / 2;
+    store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[12]) + boff, qk);
+    store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[13]) + boff, qv);
+    if ((lane & (lpg - 1)) == 0) {
+      const int64_t si = orow * (LPR / lpg) + lane / lpg;
+      store_scalar<DT>(bk.p[14], si, sk);
+      store_scalar<DT>(bk.p[15], si, sv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 fast path. Same results as pack_row<SI_DT_BF16> with fewer VALU
+// instructions per element (the pack kernel is VALU-bound):
+//  * |x| maxima on raw bf16 bit patterns with packed 16-bit integer max (the
+//    abs bit patterns order like the values; NaN patterns order above inf, so
+//    a NaN still wins), butterflies inside 16-lane rows by DPP;
+//  * scale = bf16(amax / d) by q0 = amax*RN(1/d) plus one fma correction, and
+//    the element quotient by r = RN(1/s) plus one fma correction; both equal
+//    correctly rounded division after the bf16 rounding and round-to-integer
+//    that follow (checked exhaustively over all bf16 inputs by
+//    tests/native/quotient_check.c);
+//  * clamp, then add 1.5*2^23: the add rounds to an integer (ties to even) and
+//    the low bits of the sum are the two's-complement code.
+// ---------------------------------------------------------------------------
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t max_abs_bf16x8(const uint32_t w[4]) {
+  u16x2 a = __builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu);
+  u16x2 b = __builtin_bit_cast(u16x2, w[1] & 0x7fff7fffu);
+  u16x2 c = __builtin_bit_cast(u16x2, w[2] & 0x7fff7fffu);
+  u16x2 d = __builtin_bit_cast(u16x2, w[3] & 0x7fff7fffu);
+  const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(a, b),
+                                            __builtin_elementwise_max(c, d));
+  return (uint32_t)(m.x > m.y ? m.x : m.y);
+}
+
+// v = max(v, v of lane ^ OFF) for a butterfly inside aligned groups of lanes.
+// OFF 1/2 are quad permutes; OFF 4/8 use the half-row / row mirrors, which pair
+// the same groups once the previous steps made each sub-group uniform.
+template <int OFF>
+__device__ __forceinline__ uint32_t bfly_max(uint32_t v) {
+  int o;
+  if constexpr (OFF == 1) o = __builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (OFF == 2) o = __builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (OFF == 4) o = __builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+  else if constexpr (OFF == 8) o = __builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
+  else o = __shfl_xor((int)v, OFF, 64);
+  return v > (uint32_t)o ? v : (uint32_t)o;
+}
+
+// Row maximum over LPR lanes; *grp receives the maximum over groups of lpg lanes.
+template <int LPR>
+__device__ __forceinline__ uint32_t row_group_max(uint32_t v, int lpg, uint32_t* grp) {
+  uint32_t g = v;
+  if constexpr (LPR > 1) { v = bfly_max<1>(v); if (lpg == 2) g = v; }
+  if constexpr (LPR > 2) { v = bfly_max<2>(v); if (lpg == 4) g = v; }
+  if constexpr (LPR > 4) { v = bfly_max<4>(v); if (lpg == 8) g = v; }
+  if constexpr (LPR > 8) { v = bfly_max<8>(v); if (lpg == 16) g = v; }
+  if constexpr (LPR > 16) { v = bfly_max<16>(v); if (lpg == 32) g = v; }
+  if constexpr (LPR > 32) { v = bfly_max<32>(v); }
+  if (lpg == LPR) g = v;
+  *grp = g;
+  return v;
+}
+
+// bf16(amax / d) with 0 -> 1; h = abs bf16 bits of amax.
+__device__ __forceinline__ float bf16_scale(uint32_t h, float d, float rd) {
+  const float a = __uint_as_float(h << 16);
+  float q;
+  if (h < 0x7f80u) {
+    const float q0 = a * rd;
+    q = __builtin_fmaf(__builtin_fmaf(-q0, d, a), rd, q0);
+  } else {
+    q = a / d;  // inf or NaN amax
+  }
+  const float s = bf16_bits_to_f32(f32_to_bf16_bits(q));
+  return s == 0.0f ? 1.0f : s;
+}
+
+constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+
+// Integer code (as the low bits of the returned word) of one bf16 value x.
+__device__ __forceinline__ uint32_t quant_bf16(float x, float s, float r, bool fast, float lo,
+                                               float hi) {
+  float q;
+  if (fast) {
+    const float q0 = x * r;
+    q = round_bf16_finite(__builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0));
+  } else {
+    q = bf16_bits_to_f32(f32_to_bf16_bits(x / s));
+  }
+  q = __builtin_amdgcn_fmed3f(q, lo, hi);
+  return __float_as_uint(q + kMagic);
+}
+
+// Low bytes of four words -> one word.
+__device__ __forceinline__ uint32_t bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+template <int LPR>
+__device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32_t wv[4], int c,
+                                              int s, int b, int B, int lane, int lpg,
+                                              const Buckets& bk) {
+  constexpr int D = 8 * LPR;
+  const int64_t orow = (int64_t)s * B + b;
+  const int64_t oel = orow * D + lane * 8;
+  if (c == SI_PREC_FP16 || c == SI_PREC_FP32) {
+    float xk[8], xv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xk[2 * i] = __uint_as_float(wk[i] << 16);
+      xk[2 * i + 1] = __uint_as_float(wk[i] & 0xffff0000u);
+      xv[2 * i] = __uint_as_float(wv[i] << 16);
+      xv[2 * i + 1] = __uint_as_float(wv[i] & 0xffff0000u);
+    }
+    if (c == SI_PREC_FP16) {
+      store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
+      store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+    } else {
+      store_f32<8>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
+      store_f32<8>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
+    }
+    return;
+  }
+  uint32_t gk, gv;
+  const uint32_t mk = row_group_max<LPR>(max_abs_bf16x8(wk), lpg, &gk);
+  const uint32_t mv = row_group_max<LPR>(max_abs_bf16x8(wv), lpg, &gv);
+  const bool i8 = (c == SI_PREC_INT8);
+  const float d = i8 ? 127.0f : 7.0f;
+  const float rd = i8 ? 0.0078740157186985016f : 0.14285714924335480f;  // RN(1/d)
+  const float sk = bf16_scale(i8 ? mk : gk, d, rd);
+  const float sv = bf16_scale(i8 ? mv : gv, d, rd);
+  const bool fk = sk >= 7.8886090522101181e-31f && sk < 3.0e38f;
+  const bool fv = sv >= 7.8886090522101181e-31f && sv < 3.0e38f;
+  const float rk = 1.0f / sk;
+  const float rv = 1.0f / sv;
+  const float lo = i8 ? -128.0f : -8.0f;
+  const float hi = i8 ? 127.0f : 7.0f;
+  uint32_t qk[8], qv[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    qk[2 * i] = quant_bf16(__uint_as_float(wk[i] << 16), sk, rk, fk, lo, hi);
+    qk[2 * i + 1] = quant_bf16(__uint_as_float(wk[i] & 0xffff0000u), sk, rk, fk, lo, hi);
+    qv[2 * i] = quant_bf16(__uint_as_float(wv[i] << 16), sv, rv, fv, lo, hi);
+    qv[2 * i + 1] = quant_bf16(__uint_as_float(wv[i] & 0xffff0000u), sv, rv, fv, lo, hi);
+  }
+  if (i8) {
+    *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(bk.p[8]) + oel) =
+        make_uint2(bytes4(qk[0], qk[1], qk[2], qk[3]), bytes4(qk[4], qk[5], qk[6], qk[7]));
+    *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(bk.p[9]) + oel) =
+        make_uint2(bytes4(qv[0], qv[1], qv[2], qv[3]), bytes4(qv[4], qv[5], qv[6], qv[7]));
+    if (lane == 0) {
+      reinterpret_cast<uint16_t*>(bk.p[10])[orow] = (uint16_t)(__float_as_uint(sk) >> 16);
+      reinterpret_cast<uint16_t*>(bk.p[11])[orow] = (uint16_t)(__float_as_uint(sv) >> 16);
+    }
+  } else {
+    // Byte = ((q0 & 0xF) << 4 | (q1 & 0xF)) ^ 0x88: the two's-complement nibble
+    // with its top bit flipped is the offset-binary nibble q + 8.
+    uint32_t bkk[4], bvv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bkk[j] = __builtin_amdgcn_ubfe(qk[2 * j], 0, 4) << 4 | __builtin_amdgcn_ubfe(qk[2 * j + 1], 0, 4);
+      bvv[j] = __builtin_amdgcn_ubfe(qv[2 * j], 0, 4) << 4 | __builtin_amdgcn_ubfe(qv[2 * j + 1], 0, 4);
+    }
+    const int64_t rb = (int64_t)B * D / 2;
+    const int64_t boff = (int64_t)s * rb + ((int64_t)b * D + lane * 8) / 2;
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(bk.p[12]) + boff) =
+        bytes4(bkk[0], bkk[1], bkk[2], bkk[3]) ^ 0x88888888u;
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(bk.p[13]) + boff) =
+        bytes4(bvv[0], bvv[1], bvv[2], bvv[3]) ^ 0x88888888u;
+    if ((lane & (lpg - 1)) == 0) {
+      const int64_t si = orow * (LPR / lpg) + lane / lpg;
+      reinterpret_cast<uint16_t*>(bk.p[14])[si] = (uint16_t)(__float_as_uint(sk) >> 16);
+      reinterpret_cast<uint16_t*>(bk.p[15])[si] = (uint16_t)(__float_as_uint(sv) >> 16);
+    }
+  }
+}
+
+template <int DT, int LPR, int U>
 __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin,
-                                                    const void* __restrict__ vin, int64_t B,
-                                                    int64_t H, int64_t S, int lpg,
-                                                    const int8_t* __restrict__ code,
+                                                    const void* __restrict__ vin, int B, int H,
+                                                    int S, int lpg, const int8_t* __restrict__ code,
                                                     const int32_t* __restrict__ slot,
                                                     Buckets bk) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int D = EPL * LPR;
-  const int64_t rows = B * H * S;
+  constexpr int RPP = 256 / LPR;  // rows per pass of the block
   const int lane = threadIdx.x % LPR;
-  const int groups = LPR / lpg;
-  const int64_t rb = B * D / 2;  // int4 bytes per entry (D even)
-  const int64_t step = (int64_t)gridDim.x * (blockDim.x / LPR);
-  for (int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR; row < rows;
-       row += step) {
-    const int64_t t = row % S;
-    const int64_t bh = row / S;
-    const int64_t h = bh % H;
-    const int64_t b = bh / H;
-    const int64_t e = t * H + h;
-    const int c = code[e];
-    if (c < 0 || c > 3) continue;
-    const int64_t s = slot[e];
-    float xk[EPL], xv[EPL];
-    load_chunk<DT>(kin, row * D + lane * EPL, xk);
-    load_chunk<DT>(vin, row * D + lane * EPL, xv);
-    const int64_t orow = s * B + b;
-    const int64_t oel = orow * D + lane * EPL;
-    if (c == SI_PREC_FP32) {
-      store_f32<EPL>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
-      store_f32<EPL>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
-      continue;
-    }
-    if (c == SI_PREC_FP16) {
-      store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
-      store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
-      continue;
-    }
-    // int8 (per row) or int4 (per group): shared arithmetic.
-    float gk = 0.0f, gv = 0.0f;
+  const int sub = threadIdx.x / LPR;
+  const int bh = blockIdx.y;
+  const int h = bh % H;
+  const int b = bh / H;
+  const int t0 = blockIdx.x * (RPP * U) + sub;
+  const int64_t row0 = (int64_t)bh * S;
+  int c[U], s[U];
+  if constexpr (DT == SI_DT_BF16) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    uint32_t wk[U][4], wv[U][4];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      gk = amax_fold(gk, xk[i]);
-      gv = amax_fold(gv, xv[i]);
-    }
-    for (int off = 1; off < lpg; off <<= 1) {
-      gk = amax_fold(gk, __shfl_xor(gk, off, 64));
-      gv = amax_fold(gv, __shfl_xor(gv, off, 64));
-    }
-    float mk = gk, mv = gv;
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPP;
+      c[u] = SI_PREC_EVICTED;
+      s[u] = 0;
+      if (t < S) {
+        const int e = t * H + h;
+        const int64_t off = ((row0 + t) * D + lane * EPL) * 2;
+        const u32x4 a = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + off));
+        const u32x4 bb = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vin) + off));
 #pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) {
-      if (off >= lpg) {
-        mk = amax_fold(mk, __shfl_xor(mk, off, 64));
-        mv = amax_fold(mv, __shfl_xor(mv, off, 64));
+        for (int i = 0; i < 4; ++i) {
+          wk[u][i] = a[i];
+          wv[u][i] = bb[i];
+        }
+        c[u] = code[e];
+        s[u] = slot[e];
       }
     }
-    const bool i8 = (c == SI_PREC_INT8);
-    const float sk = quant_scale<DT>(i8 ? mk : gk, i8 ? 127.0f : 7.0f);
-    const float sv = quant_scale<DT>(i8 ? mv : gv, i8 ? 127.0f : 7.0f);
-    const bool fk = sk >= 7.8886090522101181e-31f;  // 2^-100
-    const bool fv = sv >= 7.8886090522101181e-31f;
-    const float rk = 1.0f / sk;
-    const float rv = 1.0f / sv;
-    const float lo = i8 ? -128.0f : -8.0f;
-    const float hi = i8 ? 127.0f : 7.0f;
-    float qk[EPL], qv[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      qk[i] = clampf(quant_quotient<DT>(xk[i], sk, rk, fk), lo, hi);
-      qv[i] = clampf(quant_quotient<DT>(xv[i], sv, rv, fv), lo, hi);
+    for (int u = 0; u < U; ++u) {
+      if (c[u] >= 0 && c[u] <= 3) pack_row_bf16<LPR>(wk[u], wv[u], c[u], s[u], b, B, lane, lpg, bk);
     }
-    if (i8) {
-      store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[8]) + oel, qk);
-      store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[9]) + oel, qv);
-      if (lane == 0) {
-        store_scalar<DT>(bk.p[10], orow, sk);
-        store_scalar<DT>(bk.p[11], orow, sv);
+  } else {
+    float xk[U][EPL], xv[U][EPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPP;
+      c[u] = SI_PREC_EVICTED;
+      s[u] = 0;
+      if (t < S) {
+        const int e = t * H + h;
+        load_chunk<DT>(kin, (row0 + t) * D + lane * EPL, xk[u]);
+        load_chunk<DT>(vin, (row0 + t) * D + lane * EPL, xv[u]);
+        c[u] = code[e];
+        s[u] = slot[e];
       }
-    } else {
-      const int64_t boff = s * rb + (b * D + lane * EPL) / 2;
-      store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[12]) + boff, qk);
-      store_i4<EPL>(reinterpret_cast<uint8_t*>(bk.p[13]) + boff, qv);
-      if ((lane & (lpg - 1)) == 0) {
-        const int64_t si = orow * groups + lane / lpg;
-        store_scalar<DT>(bk.p[14], si, sk);
-        store_scalar<DT>(bk.p[15], si, sv);
-      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c[u] >= 0 && c[u] <= 3) pack_row<DT, LPR>(xk[u], xv[u], c[u], s[u], b, B, lane, lpg, bk);
     }
   }
 }
@@ -374,6 +593,54 @@ __global__ __launch_bounds__(256) void kv_unpack_generic(const int8_t* __restric
     }
     ok[i] = vk;
     ov[i] = vv;
+  }
+}
+
+// Unpack for D in {64, 128}: blockIdx.y = b*H + h, blockIdx.x = tile of
+// RPP*U tokens; each thread dequantizes one 4-value chunk of U rows (all loads
+// issued before the stores) and writes 16-byte non-temporal stores.
+template <int D, int SDT, int U>
+__global__ __launch_bounds__(256) void kv_unpack_fast(const int8_t* __restrict__ code,
+                                                      const int32_t* __restrict__ slot, Buckets bk,
+                                                      int B, int H, int S, int g,
+                                                      float* __restrict__ ok,
+                                                      float* __restrict__ ov) {
+  constexpr int CPR = D / 4;      // 16-byte output chunks per row
+  constexpr int RPP = 256 / CPR;  // rows per pass of the block
+  const int ch = threadIdx.x % CPR;
+  const int sub = threadIdx.x / CPR;
+  const int bh = blockIdx.y;
+  const int h = bh % H;
+  const int b = bh / H;
+  const int t0 = blockIdx.x * (RPP * U) + sub;
+  float4 rk[U], rv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + u * RPP;
+    rk[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    rv[u] = rk[u];
+    if (t < S) {
+      const int e = t * H + h;
+      const int c = code[e];
+      if (c >= 0 && c <= 3) {
+        const int s = slot[e];
+        rk[u] = dequant4<SDT>(bk, 0, c, s, b, ch * 4, B, D, g);
+        rv[u] = dequant4<SDT>(bk, 1, c, s, b, ch * 4, B, D, g);
+      }
+    }
+  }
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int64_t row0 = (int64_t)bh * S;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + u * RPP;
+    if (t < S) {
+      const int64_t off = (row0 + t) * D + ch * 4;
+      __builtin_nontemporal_store(f32x4{rk[u].x, rk[u].y, rk[u].z, rk[u].w},
+                                  reinterpret_cast<f32x4*>(ok + off));
+      __builtin_nontemporal_store(f32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w},
+                                  reinterpret_cast<f32x4*>(ov + off));
+    }
   }
 }
 
@@ -535,19 +802,20 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
                 int64_t g, const int8_t* code, const int32_t* slot, const Buckets& bk,
                 hipStream_t st) {
   constexpr int EPL = Chunk<DT>::EPL;
-  const int64_t rows = B * H * S;
+  constexpr int U = 2;
   const int64_t lpr = D / EPL;
   const int64_t lpg = g / EPL;
   const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
-  const bool fast = aligned && D % EPL == 0 && pow2(lpr) && lpr <= 64 && lpr >= 1 &&
-                    g % EPL == 0 && pow2(lpg) && lpg <= lpr && (lpr == 8 || lpr == 16 ||
-                                                                 lpr == 32 || lpr == 64 ||
-                                                                 lpr == 4);
+  const bool small = B * H < 65536 && S * H < ((int64_t)1 << 31) && B * H * S * D < ((int64_t)1 << 40);
+  const bool fast = aligned && small && D % EPL == 0 && pow2(lpr) && lpr >= 4 && lpr <= 64 &&
+                    g % EPL == 0 && pow2(lpg) && lpg <= lpr;
   if (fast) {
-    const unsigned grid = grid_for(rows * lpr, 256);
-#define SI_PACK_CASE(L)                                                                      \
-  case L:                                                                                    \
-    kv_pack_fast<DT, L><<<grid, 256, 0, st>>>(k, v, B, H, S, (int)lpg, code, slot, bk);      \
+    const int rpb = (int)(256 / lpr) * U;
+    const dim3 grid((unsigned)ceil_div(S, rpb), (unsigned)(B * H));
+#define SI_PACK_CASE(L)                                                                     \
+  case L:                                                                                   \
+    kv_pack_fast<DT, L, U><<<grid, 256, 0, st>>>(k, v, (int)B, (int)H, (int)S, (int)lpg,    \
+                                                 code, slot, bk);                           \
     break;
     switch (lpr) {
       SI_PACK_CASE(4)
@@ -561,6 +829,28 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
   }
   kv_pack_generic<DT><<<grid_for(S * H, 256), 256, 0, st>>>(k, v, B, H, S, D, g, code, slot, bk);
   return check_launch("si_kv_pack/generic");
+}
+
+template <int D>
+void launch_unpack_fast(int sdt, const int8_t* code, const int32_t* slot, const Buckets& bk,
+                        int64_t B, int64_t H, int64_t S, int64_t g, float* ok, float* ov,
+                        hipStream_t st) {
+  constexpr int U = 4;
+  constexpr int rpb = (256 / (D / 4)) * U;
+  const dim3 grid((unsigned)ceil_div(S, rpb), (unsigned)(B * H));
+  switch (sdt) {
+    case SI_DT_F32:
+      kv_unpack_fast<D, SI_DT_F32, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S,
+                                                            (int)g, ok, ov);
+      break;
+    case SI_DT_F16:
+      kv_unpack_fast<D, SI_DT_F16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S,
+                                                            (int)g, ok, ov);
+      break;
+    default:
+      kv_unpack_fast<D, SI_DT_BF16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H,
+                                                             (int)S, (int)g, ok, ov);
+  }
 }
 
 }  // namespace
@@ -602,6 +892,14 @@ extern "C" int si_kv_unpack(const int8_t* code, const int32_t* slot, const void*
   hipStream_t st = as_stream(stream);
   const bool vec = D % 4 == 0 && group % 4 == 0 &&
                    ((reinterpret_cast<uintptr_t>(out_k) | reinterpret_cast<uintptr_t>(out_v)) & 15) == 0;
+  const bool small = B * H < 65536 && S * H < ((int64_t)1 << 31) && group < ((int64_t)1 << 31);
+  if (vec && small && (D == 128 || D == 64)) {
+    if (D == 128)
+      launch_unpack_fast<128>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
+    else
+      launch_unpack_fast<64>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
+    return check_launch("si_kv_unpack/fast");
+  }
   if (vec) {
     const unsigned grid = grid_for(total / 4, 256);
     switch (scale_dtype) {
