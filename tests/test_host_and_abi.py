@@ -1,0 +1,215 @@
+"""CPU tests: the C-ABI library loads and exports every entry point of
+include/shadowinfer_hip.h, argument validation fails cleanly without a GPU,
+and the host-side logic of the Python mirror (codes <-> map, CPU plans,
+grouping rules, validation and error behaviour) matches the reference."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import oracle as O
+from shadowinfer_amd import _native, get_kernel_status
+from shadowinfer_amd.ffn_optimizer import INT8Linear, quantize_ffn_modules
+from shadowinfer_amd.shadowkv import (PRECISION_CODES, PackedKVCache, PrecisionPlan, codes_to_map,
+                                      map_to_codes, packed_attention)
+from shadowinfer_amd.shadowkv.packed_kv_cache import _pack_codes_from_map
+from shadowinfer_amd.utils import Quantizer
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "shadowinfer_hip.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(si_[a-z0-9_]+)\s*\(", text)))
+
+
+# ------------------------------------------------------------------- ABI
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    declared = _header_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert sorted(_native.EXPORTED_SYMBOLS) == declared
+
+
+def test_abi_version_and_status():
+    version = int(re.search(r"#define SI_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert _native.load().si_abi_version() == version
+    st = get_kernel_status()
+    assert st["hip_extensions_loaded"] and st["abi_version"] == version
+    assert st["cpu_fallback"] is False and st["kv_pack_kernel"] == "hip"
+
+
+def test_argument_validation_needs_no_device():
+    """Invalid arguments are rejected before any HIP call, with a message."""
+    lib = _native.load()
+    null = None
+    table = _native.table16([None] * 16)
+    rc = lib.si_kv_pack(1, 1, 2, 1, 2, 8, 64, 24, 1, 1, table, null)  # 24 does not divide 64
+    assert rc == 1 and b"group" in lib.si_last_error()
+    assert lib.si_kv_pack(1, 1, 7, 1, 2, 8, 64, 16, 1, 1, table, null) == 1  # bad dtype
+    assert lib.si_act_quant_i8(1, 9, 4, 4, 1, 1, null) == 1
+    ws = _native.size_query("si_plan_workspace_bytes", 100)
+    assert lib.si_plan_scan(1, null, 100, 1, 1, 1, 1, ws - 1, null) == 1
+    assert b"workspace" in lib.si_last_error()
+    rc = lib.si_attn_packed_fwd(1, 2, 1, 1, 8, 96, 1, 1, table, 2, 8, 16, ctypes.c_float(0.1), 1, 0, null)
+    assert rc == 1 and b"head_dim" in lib.si_last_error()
+    assert lib.si_int4_unpack_rows(1, 1, 2, 5, 1, null) == 1  # 2 bytes hold at most 4 codes
+    with pytest.raises(ValueError, match="si_kv_unpack"):
+        _native.call("si_kv_unpack", 1, 1, table, 2, 1, 1, 1, 64, 48, 1, 1, None)
+
+
+def test_workspace_queries():
+    assert _native.size_query("si_gemm_workspace_bytes", 16, 11008, 4096) > 0  # split-K
+    assert _native.size_query("si_gemm_workspace_bytes", 2048, 11008, 4096) == 0
+    assert _native.size_query("si_int8_linear_workspace_bytes", 16, 4096, 11008) >= 16 * 4096
+
+
+# ------------------------------------------------------- codes and plans
+def test_map_to_codes_and_back_match_reference_semantics():
+    pm = {0: {0: "fp32", 2: "evicted"}, 1: {1: "INT8"}, 2: {0: "int4", 1: "fp16", 2: "fp32"},
+          4: {2: "evicted"}}
+    codes = map_to_codes(pm, 5, 3)
+    assert codes.dtype == torch.int8 and codes.shape == (5, 3)
+    np.testing.assert_array_equal(codes.numpy(), O.map_to_codes(pm, 5, 3))
+    back = codes_to_map(codes)
+    assert back[0] == {0: "fp32", 1: "fp16", 2: "evicted"} and back[3] == {0: "fp16", 1: "fp16", 2: "fp16"}
+    with pytest.raises(ValueError):
+        map_to_codes({0: {0: "bf16"}}, 1, 1, strict=True)
+    assert int(map_to_codes({0: {0: "bf16"}}, 1, 1, strict=False)[0, 0]) == PRECISION_CODES["fp16"]
+    with pytest.raises(ValueError):
+        codes_to_map(torch.tensor([[7]], dtype=torch.int8))
+
+
+def test_cpu_plan_matches_oracle():
+    rng = np.random.default_rng(3)
+    for S, H in ((1, 1), (5, 3), (64, 4), (300, 7)):
+        codes = rng.integers(-1, 6, size=(S, H)).astype(np.int8)
+        mask = {(int(t), int(h)): bool(rng.random() < 0.4) for t in range(S) for h in range(H)}
+        mask[(S + 3, 0)] = True  # out of range -> ignored
+        plan = PrecisionPlan.from_codes(torch.from_numpy(codes), reuse_mask=mask)
+        ref = O.plan_from_codes(codes, mask)
+        assert plan.groups == ref["groups"]
+        for p in ("fp32", "fp16", "int8", "int4"):
+            np.testing.assert_array_equal(plan.flat_indices[p].numpy(), ref["flat_indices"][p])
+        assert plan.evicted_entries == ref["evicted_entries"]
+        assert plan.reuse_entries == ref["reuse_entries"]
+        assert plan.fingerprint == ref["fingerprint"]
+        assert plan.reuse_set() == set(ref["reuse_entries"])
+
+
+def test_plan_build_equals_from_codes_and_is_immutable():
+    names = ("fp32", "fp16", "int8", "int4")
+    pm = {t: {h: names[(t + h) % 4] for h in range(3)} for t in range(6)}
+    built = PrecisionPlan.build(pm, 6, 3, reuse_mask={(1, 1): True})
+    other = PrecisionPlan.from_codes(map_to_codes(pm, 6, 3), reuse_mask={(1, 1): True})
+    assert built.groups == other.groups and built.fingerprint == other.fingerprint
+    with pytest.raises(AttributeError):
+        built.seq_len = 3
+    with pytest.raises(ValueError):
+        PrecisionPlan.from_codes(torch.zeros(4, dtype=torch.int8))
+    with pytest.raises(ValueError):
+        PrecisionPlan.from_codes(torch.zeros(0, 3, dtype=torch.int8))
+    with pytest.raises(ValueError):
+        PrecisionPlan.build({1: {1: "bf16"}}, 2, 2, strict=True)
+    with pytest.raises(ValueError):
+        built.device_grouping()  # a CPU plan cannot drive a device pack
+
+
+def test_pack_map_grouping_rules():
+    rng = np.random.default_rng(9)
+    names = ["fp32", "FP16", "int8", "int4", "evicted", "bf16", "weird"]
+    pm = {t: {h: names[rng.integers(0, len(names))] for h in range(4) if rng.random() < 0.8}
+          for t in range(20) if rng.random() < 0.9}
+    np.testing.assert_array_equal(_pack_codes_from_map(pm, 20, 4).reshape(20, 4),
+                                  O.pack_map_to_codes(pm, 20, 4))
+
+
+# ----------------------------------------------------- error behaviour
+def test_cpu_tensors_fail_loudly():
+    k = torch.randn(1, 2, 4, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        PackedKVCache.pack(k, k, {})
+    with pytest.raises(RuntimeError, match="HIP device"):
+        Quantizer.quantize_int8(k)
+    layer = INT8Linear(torch.zeros(64, 32, dtype=torch.int8), torch.ones(32))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        layer(torch.randn(3, 64))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        INT8Linear.from_linear(nn.Linear(8, 8))
+
+
+def test_empty_cache_is_safe_without_device():
+    """reference tests/test_kv_store.py:528-552 (UT-12.10)."""
+    packed = PackedKVCache(1, 2, 8, 64)
+    k, v = packed.unpack()
+    assert k.shape == (1, 2, 8, 64) and torch.count_nonzero(k) == 0 and torch.count_nonzero(v) == 0
+    assert packed.evict({(0, 0)}) == 0
+    assert packed.memory_bytes() == 0 and packed.resident_bytes() == 0
+    assert packed.packed_data == {}
+    assert packed.apply_reuse_mask(PackedKVCache(1, 2, 8, 64), {(0, 0): True}, return_stats=True) == \
+        {"applied": 0, "skipped_precision": 0}
+    with pytest.raises(ValueError):
+        packed.apply_reuse_mask(PackedKVCache(1, 2, 8, 32), {(0, 0): True})
+    assert "PackedKVCache(batch=1" in repr(packed)
+
+
+def test_int8_linear_validation_and_accounting():
+    """reference tests/test_int8_ffn.py:114-152."""
+    layer = INT8Linear(torch.zeros(128, 96, dtype=torch.int8), torch.ones(96), bias=torch.zeros(96))
+    assert layer(torch.empty(0, 128)).shape == (0, 96)
+    with pytest.raises(ValueError):
+        layer(torch.randn(4, 127))
+    with pytest.raises(ValueError):
+        INT8Linear(torch.zeros(128, dtype=torch.int8), torch.ones(96))
+    with pytest.raises(ValueError):
+        INT8Linear(torch.zeros(128, 96, dtype=torch.int8), torch.ones(95))
+    with pytest.raises(ValueError):
+        INT8Linear(torch.zeros(128, 96, dtype=torch.int8), torch.ones(96), bias=torch.zeros(95))
+    with pytest.raises(ValueError):
+        INT8Linear(torch.zeros(128, 96, dtype=torch.int16), torch.ones(96))
+    assert layer.memory_bytes() == 128 * 96 + 4 * 96 + 4 * 96
+    assert layer.dense_equivalent_bytes() == 4 * 128 * 96 + 4 * 96
+    nobias = INT8Linear(torch.zeros(128, 96, dtype=torch.int8), torch.ones(96))
+    assert nobias.dense_equivalent_bytes() / nobias.memory_bytes() >= 3.8
+    assert layer.qweight.dtype == torch.int8 and layer.weight_scale.dtype == torch.float32
+    assert set(layer.state_dict()) == {"qweight", "weight_scale", "bias"}
+    with pytest.raises(TypeError):
+        INT8Linear.from_linear(nn.Conv1d(2, 2, 1))
+    assert quantize_ffn_modules(nn.Sequential(nn.Linear(4, 4))) == {"supported": False}
+
+
+def test_quantizer_host_rules():
+    with pytest.raises(ValueError):
+        Quantizer.quantize_tensor(torch.randn(10), "int2")
+    with pytest.raises(ValueError):
+        Quantizer.dequantize_tensor(torch.zeros(10, dtype=torch.int8), None, "int8")
+    with pytest.raises(ValueError):
+        Quantizer.dequantize_tensor(torch.zeros(10, 2, dtype=torch.int8), None, "int4")
+    x = torch.randn(10, 20)
+    q, s = Quantizer.quantize_tensor(x, "fp32")
+    assert q is x and s is None
+    q, s = Quantizer.quantize_tensor(x, "fp16")
+    assert q.dtype == torch.float16 and s is None
+    q, s = Quantizer.quantize_int8(torch.empty(0))
+    assert q.numel() == 0 and float(s) == 1.0
+    assert Quantizer.pack_int4(torch.empty(0, dtype=torch.int8)).numel() == 0
+    assert Quantizer.unpack_int4(torch.empty(0, dtype=torch.uint8), (2, 3)).shape == (2, 3)
+
+
+def test_packed_attention_validation():
+    cache = PackedKVCache(1, 2, 16, 64)
+    with pytest.raises(ValueError):
+        packed_attention(torch.randn(1, 3, 8, 64, dtype=torch.bfloat16), cache)
+    with pytest.raises(ValueError):
+        packed_attention(torch.randn(8, 64, dtype=torch.bfloat16), cache)
+    with pytest.raises(TypeError):
+        packed_attention(torch.randn(1, 2, 8, 64), cache)
