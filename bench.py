@@ -202,8 +202,8 @@ def bench_gemm(torch, dev, iters=50):
     K, N = 4096, 11008
     gen = torch.Generator(device=dev).manual_seed(7)
     copies = 8  # 8 x 45 MB of weights: more than the 256 MB last-level cache
-    ws = [torch.randint(-127, 128, (K, N), generator=gen, device=dev, dtype=torch.int8)
-          for _ in range(copies)]
+    ws = [torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+          for _ in range(copies)]  # [N, K]: nn.Linear layout, as INT8Linear keeps it
     sw = torch.rand(N, generator=gen, device=dev) * 1e-3 + 1e-4
     timer = EventTimer(torch, stream)
     out = {}

@@ -180,7 +180,9 @@ int si_dequant_rows(const int8_t* q, const void* scale, int scale_dtype, int64_t
 /* ---------------------------------------------------------------------- */
 
 /* INT8Linear.from_linear (ffn_optimizer/int8_linear.py:65-82):
- * w fp32 [N, K] -> qweight int8 [K, N] (transposed), scale fp32 [N]. */
+ * w fp32 [N, K] -> qweight int8 [N, K], scale fp32 [N]. The quantized weight
+ * keeps nn.Linear's [N, K] layout (K contiguous, the MFMA fragment layout);
+ * the reference's stored [K, N] tensor is its transpose. */
 int si_weight_quant_i8(const float* w, int64_t N, int64_t K, int8_t* qweight,
                        float* scale, si_stream_t stream);
 
@@ -193,13 +195,15 @@ int si_act_quant_i8(const void* x, int dtype, int64_t M, int64_t K, int8_t* q,
  * partial sums; 0 when the shape runs without splitting). */
 size_t si_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
-/* torch._int_mm (int8_linear.py:102): a int8 [M, K] x b int8 [K, N] ->
- * c int32 [M, N], exact. */
+/* torch._int_mm (int8_linear.py:102): c[m, n] = sum_k a[m, k] * b[n, k],
+ * a int8 [M, K], b int8 [N, K] (the weight in [N, K] layout), c int32 [M, N],
+ * exact. */
 int si_gemm_i8i8_i32(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K,
                      int32_t* c, void* workspace, size_t workspace_bytes, si_stream_t stream);
 
 /* _int_mm + epilogue (int8_linear.py:102-115): out[m, n] =
- * T(float(acc) * (sx[m] * sw[n]) [+ bias[n]]), T = out_dtype. bias optional. */
+ * T(float(acc) * (sx[m] * sw[n]) [+ bias[n]]), T = out_dtype, b int8 [N, K].
+ * bias optional. */
 int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t* b, const float* sw,
                        const float* bias, int64_t M, int64_t N, int64_t K, void* out,
                        int out_dtype, void* workspace, size_t workspace_bytes,
@@ -210,7 +214,8 @@ int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t* b, const 
 size_t si_int8_linear_workspace_bytes(int64_t M, int64_t K, int64_t N);
 
 /* Whole INT8Linear.forward on a 2-D input (int8_linear.py:88-115):
- * activation quantization, int8 GEMM, epilogue. out [M, N] in dtype. */
+ * activation quantization, int8 GEMM, epilogue. qweight int8 [N, K];
+ * out [M, N] in dtype. */
 int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64_t N,
                            const int8_t* qweight, const float* sw, const float* bias,
                            void* out, void* workspace, size_t workspace_bytes,

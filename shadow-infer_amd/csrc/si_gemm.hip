@@ -1,32 +1,40 @@
-// int8 x int8 -> int32 GEMM on gfx950 MFMA (v_mfma_i32_16x16x64_i8) with the
-// INT8Linear dequant epilogue (ffn_optimizer/int8_linear.py:102-115).
+// int8 x int8 -> int32 GEMM on gfx950 MFMA with the INT8Linear dequant
+// epilogue (ffn_optimizer/int8_linear.py:102-115).
 //
-// Operands: A = quantized activations [M, K] (K contiguous), B = qweight
-// [K, N] (N contiguous, the reference's stored layout). MFMA wants K-contiguous
-// fragments for both operands, so the B tile is transposed while it is staged:
-// each thread loads a 4(k) x 16(n) byte block with four 16-byte loads,
-// transposes it in registers with byte permutes and writes 16 dwords of
-// 4 consecutive k to the LDS tile Bs[n][k].
+// Operands: A = quantized activations [M, K], B = quantized weight [N, K]
+// (nn.Linear's layout). Both are K-contiguous, which is the register layout
+// of MFMA fragments, so tiles move as 16-byte chunks with no transposition.
 //
-// Fragment layout of v_mfma_i32_16x16x64_i8: lane l holds row (l % 16) of A
-// and column (l % 16) of B, each as 16 consecutive k values starting at
-// 16 * (l / 16); the accumulator lane l holds C[4*(l/16) + r][l % 16], r < 4.
-// The k order inside a fragment only has to agree between A and B, which it
-// does by construction, so the int32 sum is exact for any order.
+// Three kernels:
+//  * gemm_dma (the default for M > 16): BM x BN x BK tiles copied global ->
+//    LDS by global_load_lds_dwordx4 into 4 LDS stages (no register staging,
+//    two k-tiles in flight behind the one being multiplied), XOR-swizzled
+//    16-byte chunks, v_mfma_i32_32x32x32_i8 on a 2x2 wave grid.
+//  * gemm_tile: the same tiling with register-staged copies into
+//    double-buffered, padded LDS; used where K is not a multiple of 64.
+//  * gemm_skinny (M <= 16): weight streaming. No LDS: every lane loads its
+//    v_mfma_i32_16x16x64_i8 fragments directly (16 bytes of one weight row,
+//    16 bytes of one activation row from L2); K is split so that enough
+//    wavefronts stream the weight to keep HBM busy.
 //
-// Split-K: when the (M, N) tile grid alone cannot fill the 256 CUs, K is split
-// over blockIdx.z; each split writes an int32 partial and a second kernel adds
-// the partials (integer adds, so the result does not depend on the order) and
-// applies the epilogue.
+// Fragment layouts: 16x16x64 - lane l holds A row (l%16) / B row (l%16), 16
+// consecutive k starting at 16*(l/16); C lane l holds rows 4*(l/16)+r, r<4, of
+// column l%16. 32x32x32 - lane l holds A/B row (l%32), 16 consecutive k
+// starting at 16*(l/32); C lane l holds rows 8*(r/4) + 4*(l/32) + r%4, r<16,
+// of column l%32. The k order inside a fragment only has to agree between A
+// and B, which it does by construction, so the int32 sums are exact.
+//
+// Split-K partial sums are int32 and are added by gemm_finalize (integer adds:
+// the result does not depend on the order).
+#include <stdlib.h>
+
 #include "si_common.h"
 
 namespace si {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-constexpr int BK = 64;         // k per staged tile = one MFMA k-step
-constexpr int LDK = BK + 16;   // LDS row pitch in bytes (padding against bank conflicts)
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 enum Epi { EPI_I32 = 0, EPI_PARTIAL = 1, EPI_DEQUANT = 2 };
 
@@ -48,129 +56,449 @@ __device__ __forceinline__ void store_dequant(const EpiArgs& ep, int64_t idx, in
   store_any(ep.out, ep.out_dtype, idx, o);
 }
 
-// 4x4 byte transpose: in[r] holds bytes (k=r, n=0..3); out[c] holds (n=c, k=0..3).
-__device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
-  // Interleave pairs of rows, then pairs of pairs (v_perm_b32 selects bytes of {a, b}).
-  const uint32_t t01_lo = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // k0n0 k1n0 k0n1 k1n1
-  const uint32_t t01_hi = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // k0n2 k1n2 k0n3 k1n3
-  const uint32_t t23_lo = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
-  const uint32_t t23_hi = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
-  out[0] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x05040100u);  // n0: k0 k1 k2 k3
-  out[1] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x07060302u);  // n1
-  out[2] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x05040100u);  // n2
-  out[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);  // n3
+template <int EPI>
+__device__ __forceinline__ void epi_store(const EpiArgs& ep, int32_t* C, int64_t M, int64_t N,
+                                          int64_t m, int64_t n, int32_t v, int split) {
+  if (EPI == EPI_I32) {
+    C[m * N + n] = v;
+  } else if (EPI == EPI_PARTIAL) {
+    ep.partial[((int64_t)split * M + m) * N + n] = v;
+  } else {
+    store_dequant(ep, m * N + n, v, ep.sx[m], ep.sw[n], ep.bias != nullptr ? ep.bias[n] : 0.0f);
+  }
 }
 
-// Requirements (checked on the host): K % 16 == 0, N % 16 == 0, k_split % BK == 0.
-template <int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(256) void gemm_i8_mfma(const int8_t* __restrict__ A,
-                                                   const int8_t* __restrict__ B, int64_t M,
-                                                   int64_t N, int64_t K, int64_t k_split,
-                                                   int32_t* __restrict__ C, EpiArgs ep) {
-  static_assert(WM * WN == 4, "four waves per block");
-  constexpr int TM = BM / WM;  // rows per wave
-  constexpr int TN = BN / WN;  // cols per wave
-  constexpr int FM = TM / 16;
-  constexpr int FN = TN / 16;
-  __shared__ __attribute__((aligned(16))) uint8_t As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[BN * LDK];
+// ---------------------------------------------------------------------------
+// Tile kernel. Requires K % BK == 0 (K per split too).
+// Pipeline: two LDS stages and two register staging sets. While the MFMAs of
+// k-tile t run from LDS stage t%2, the global loads of k-tile t+2 are in
+// flight and k-tile t+1 waits in registers to be stored into the other stage
+// after the MFMAs. Within a k-tile the fragments of k-step s+1 are read from
+// LDS before the MFMAs of k-step s are issued.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK>
+struct TileCfg {
+  static constexpr int P = BK + 16;  // LDS row pitch in bytes
+  static constexpr int CPR = BK / 16;
+  static constexpr int ACH = BM * CPR / 256;
+  static constexpr int BCH = BN * CPR / 256;
+  static constexpr int STAGE = (BM + BN) * P;
+};
 
+template <int BM, int BN, int BK>
+__device__ __forceinline__ void tile_gload(v4i* ra, v4i* rb, const int8_t* __restrict__ A,
+                                           const int8_t* __restrict__ B, int M, int N, int K,
+                                           int m0, int n0, int k0) {
+  using C = TileCfg<BM, BN, BK>;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t n0 = (int64_t)blockIdx.x * BN;
-  const int64_t kb = (int64_t)blockIdx.z * k_split;
-  const int64_t ke = kb + k_split < K ? kb + k_split : K;
+#pragma unroll
+  for (int i = 0; i < C::ACH; ++i) {
+    const int c = tid + i * 256;
+    const int m = m0 + c / C::CPR;
+    ra[i] = m < M ? *reinterpret_cast<const v4i*>(A + (int64_t)m * K + k0 + (c % C::CPR) * 16)
+                  : v4i{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int i = 0; i < C::BCH; ++i) {
+    const int c = tid + i * 256;
+    const int n = n0 + c / C::CPR;
+    rb[i] = n < N ? *reinterpret_cast<const v4i*>(B + (int64_t)n * K + k0 + (c % C::CPR) * 16)
+                  : v4i{0, 0, 0, 0};
+  }
+}
 
-  v4i acc[FM][FN];
+template <int BM, int BN, int BK>
+__device__ __forceinline__ void tile_sstore(int8_t* stage, const v4i* ra, const v4i* rb) {
+  using C = TileCfg<BM, BN, BK>;
+  const int tid = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < C::ACH; ++i) {
+    const int c = tid + i * 256;
+    *reinterpret_cast<v4i*>(stage + (c / C::CPR) * C::P + (c % C::CPR) * 16) = ra[i];
+  }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  for (int i = 0; i < C::BCH; ++i) {
+    const int c = tid + i * 256;
+    *reinterpret_cast<v4i*>(stage + (BM + c / C::CPR) * C::P + (c % C::CPR) * 16) = rb[i];
+  }
+}
 
-  for (int64_t k0 = kb; k0 < ke; k0 += BK) {
-    // ---- stage A: BM rows x 64 bytes, 16-byte vectors ----
-    for (int i = tid; i < BM * 4; i += 256) {
-      const int r = i >> 2;
-      const int q = i & 3;
-      const int64_t m = m0 + r;
-      const int64_t k = k0 + q * 16;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m < M && k < ke) v = *reinterpret_cast<const uint4*>(A + m * K + k);
-      *reinterpret_cast<uint4*>(As + r * LDK + q * 16) = v;
+template <int BM, int BN, int BK, int WM, int WN>
+__device__ __forceinline__ void tile_compute(const int8_t* stage, v16i (*acc)[BN / WN / 32],
+                                             int wm, int wn, int lane) {
+  using C = TileCfg<BM, BN, BK>;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int KS = BK / 32;
+  const int8_t* As = stage + (wm * TM + (lane & 31)) * C::P + (lane >> 5) * 16;
+  const int8_t* Bs = stage + (BM + wn * TN + (lane & 31)) * C::P + (lane >> 5) * 16;
+  v4i af[2][FM], bf[2][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const v4i*>(As + i * 32 * C::P);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) bf[0][j] = *reinterpret_cast<const v4i*>(Bs + j * 32 * C::P);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int cur = ks & 1;
+    if (ks + 1 < KS) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[cur ^ 1][i] = *reinterpret_cast<const v4i*>(As + i * 32 * C::P + (ks + 1) * 32);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[cur ^ 1][j] = *reinterpret_cast<const v4i*>(Bs + j * 32 * C::P + (ks + 1) * 32);
     }
-    // ---- stage B: 64 x BN bytes as 4x16 blocks, transposed to Bs[n][k] ----
-    for (int i = tid; i < 16 * (BN / 16); i += 256) {
-      const int kq = i / (BN / 16);  // 0..15: 4-row group
-      const int nq = i % (BN / 16);  // 16-column group
-      const int64_t k = k0 + kq * 4;
-      const int64_t n = n0 + nq * 16;
-      uint4 rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        rows[r] = make_uint4(0, 0, 0, 0);
-        if (n < N && k + r < ke) rows[r] = *reinterpret_cast<const uint4*>(B + (k + r) * N + n);
-      }
-      const uint32_t* rw = reinterpret_cast<const uint32_t*>(rows);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {  // 4 columns per dword
-        const uint32_t in[4] = {rw[0 * 4 + c], rw[1 * 4 + c], rw[2 * 4 + c], rw[3 * 4 + c]};
-        uint32_t out[4];
-        transpose4x4(in, out);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<uint32_t*>(Bs + (nq * 16 + c * 4 + j) * LDK + kq * 4) = out[j];
-      }
-    }
-    __syncthreads();
-    // ---- MFMA ----
-    v4i af[FM], bf[FN];
-    const int fr = lane & 15;
-    const int fk = (lane >> 4) * 16;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[i] = *reinterpret_cast<const v4i*>(As + (wm * TM + i * 16 + fr) * LDK + fk);
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn * TN + j * 16 + fr) * LDK + fk);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// Dequant store with the output dtype fixed at compile time.
+template <int ODT>
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
+  if (ODT == SI_DT_F32) {
+    reinterpret_cast<float*>(out)[idx] = v;
+  } else {
+    const uint32_t h = ODT == SI_DT_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+    reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)h;
+  }
+}
+
+// EPI: EPI_I32 / EPI_PARTIAL; EPI_DEQUANT + 16 * out dtype for the dequant epilogue.
+template <int BM, int BN, int BK, int WM, int WN, int EPI>
+__global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
+                                                 const int8_t* __restrict__ B, int M, int N, int K,
+                                                 int k_split, int32_t* __restrict__ Cout,
+                                                 EpiArgs ep) {
+  static_assert(WM * WN == 4, "four waves per block");
+  using C = TileCfg<BM, BN, BK>;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  static_assert(C::ACH * 256 == BM * C::CPR && C::BCH * 256 == BN * C::CPR, "chunks per thread");
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * C::STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int kb = blockIdx.z * k_split;
+  const int ke = min(kb + k_split, K);
+  const int nk = (ke - kb) / BK;
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  v4i ra0[C::ACH], rb0[C::BCH], ra1[C::ACH], rb1[C::BCH];
+  int8_t* s0 = lds;
+  int8_t* s1 = lds + C::STAGE;
+  if (nk > 0) tile_gload<BM, BN, BK>(ra0, rb0, A, B, M, N, K, m0, n0, kb);
+  if (nk > 1) tile_gload<BM, BN, BK>(ra1, rb1, A, B, M, N, K, m0, n0, kb + BK);
+  if (nk > 0) tile_sstore<BM, BN, BK>(s0, ra0, rb0);
+  __syncthreads();
+  for (int it = 0; it < nk; it += 2) {
+    if (it + 2 < nk) tile_gload<BM, BN, BK>(ra0, rb0, A, B, M, N, K, m0, n0, kb + (it + 2) * BK);
+    tile_compute<BM, BN, BK, WM, WN>(s0, acc, wm, wn, lane);
+    if (it + 1 < nk) tile_sstore<BM, BN, BK>(s1, ra1, rb1);
+    __syncthreads();
+    if (it + 1 >= nk) break;
+    if (it + 3 < nk) tile_gload<BM, BN, BK>(ra1, rb1, A, B, M, N, K, m0, n0, kb + (it + 3) * BK);
+    tile_compute<BM, BN, BK, WM, WN>(s1, acc, wm, wn, lane);
+    if (it + 2 < nk) tile_sstore<BM, BN, BK>(s0, ra0, rb0);
     __syncthreads();
   }
 
-  // ---- epilogue ----
-  const int col = lane & 15;
-  const int rq = (lane >> 4) * 4;
+  const int col = lane & 31;
+  const int rq = (lane >> 5) * 4;
+  constexpr int KIND = EPI & 15;
+  constexpr int ODT = EPI >> 4;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + j * 32 + col;
+    if (n >= N) continue;
+    float sw = 0.0f, bias = 0.0f;
+    if (KIND == EPI_DEQUANT) {
+      sw = ep.sw[n];
+      if (ep.bias != nullptr) bias = ep.bias[n];
+    }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + wn * TN + j * 16 + col;
-      if (n >= N) continue;
-      float sw = 0.0f, bias = 0.0f;
-      if (EPI == EPI_DEQUANT) {
-        sw = ep.sw[n];
-        if (ep.bias != nullptr) bias = ep.bias[n];
-      }
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * TM + i * 16 + rq + r;
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + rq + (r & 3);
         if (m >= M) continue;
         const int32_t v = acc[i][j][r];
-        if (EPI == EPI_I32) {
-          C[m * N + n] = v;
-        } else if (EPI == EPI_PARTIAL) {
-          ep.partial[((int64_t)blockIdx.z * M + m) * N + n] = v;
+        const int64_t idx = (int64_t)m * N + n;
+        if (KIND == EPI_I32) {
+          Cout[idx] = v;
+        } else if (KIND == EPI_PARTIAL) {
+          ep.partial[(int64_t)blockIdx.z * M * N + idx] = v;
         } else {
-          store_dequant(ep, m * N + n, v, ep.sx[m], sw, bias);
+          float o = (float)v * (ep.sx[m] * sw);
+          if (ep.bias != nullptr) o = o + bias;
+          store_out<ODT>(ep.out, idx, o);
         }
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// DMA tile kernel: global -> LDS copies by global_load_lds_dwordx4 (no register
+// staging), S LDS stages, so k-tiles t+1 .. t+S-2 are in flight while the
+// MFMAs of k-tile t run. One wave instruction fills 1 KB of LDS, lane l the
+// 16 bytes at 16*l: rows of a stage are therefore unpadded (BK bytes) and the
+// 16-byte chunks of row r are stored at slot chunk ^ swz(r); swz spreads the
+// rows read by one fragment load over distinct banks (32- and 64-bank LDS).
+// Requires K % BK == 0 (K per split too) and 16-byte aligned operands.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+
+template <int CPR>
+__device__ __forceinline__ int chunk_swz(int r) {
+  if constexpr (CPR == 4) return ((r >> 1) ^ (r >> 2)) & 3;
+  else return (r ^ (r >> 1)) & 7;
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int S, int EPI>
+__global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
+                                                const int8_t* __restrict__ B, int M, int N, int K,
+                                                int k_split, int32_t* __restrict__ Cout,
+                                                EpiArgs ep) {
+  static_assert(WM * WN == 4, "four waves per block");
+  constexpr int CPR = BK / 16;
+  constexpr int LA = BM * BK / 1024 / 4;  // 1-KB DMA blocks of A per wave per k-tile
+  constexpr int LB = BN * BK / 1024 / 4;
+  static_assert(LA * 4096 == BM * BK && LB * 4096 == BN * BK, "whole DMA blocks per wave");
+  constexpr int LPT = LA + LB;            // vm loads per thread per k-tile
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int KS = BK / 32;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int kb = blockIdx.z * k_split;
+  const int ke = min(kb + k_split, K);
+  const int nk = (ke - kb) / BK;
+
+  // Source of the 16 bytes this lane copies into each of its DMA blocks.
+  const int8_t* asrc[LA];
+  const int8_t* bsrc[LB];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int p = (i * 4 + wave) * 1024 + 16 * lane;
+    const int r = p / BK;
+    const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
+    const int m = min(m0 + r, M - 1);  // rows past M feed only discarded outputs
+    asrc[i] = A + (int64_t)m * K + kb + 16 * c;
+  }
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int p = (i * 4 + wave) * 1024 + 16 * lane;
+    const int r = p / BK;
+    const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
+    const int n = min(n0 + r, N - 1);
+    bsrc[i] = B + (int64_t)n * K + kb + 16 * c;
+  }
+  auto issue = [&](int t) {
+    int8_t* st = lds + (t % S) * STAGE;
+    const int k0 = t * BK;
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid_t*)(asrc[i] + k0),
+                                       (lvoid_t*)(st + (i * 4 + wave) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid_t*)(bsrc[i] + k0),
+                                       (lvoid_t*)(st + BM * BK + (i * 4 + wave) * 1024), 16, 0, 0);
+  };
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  // Fragment rows of this lane and their swizzles (fixed across k-tiles).
+  int arow[FM], asw[FM], brow[FN], bsw[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int r = wm * TM + i * 32 + (lane & 31);
+    arow[i] = r * BK;
+    asw[i] = chunk_swz<CPR>(r);
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int r = wn * TN + j * 32 + (lane & 31);
+    brow[j] = BM * BK + r * BK;
+    bsw[j] = chunk_swz<CPR>(r);
+  }
+  const int khalf = lane >> 5;
+
+  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
+  for (int t = 0; t < nk; ++t) {
+    const int rem = min(nk - 1 - t, S - 2);
+    if (rem >= S - 2) wait_vmcnt<(S - 2) * LPT>();
+    else if (S > 3 && rem == 1) wait_vmcnt<LPT>();
+    else wait_vmcnt<0>();
+    // Bare barrier: this wave's copies of k-tile t are complete (waited
+    // above) and its LDS reads of k-tile t-1 have returned (the MFMAs that
+    // consumed them were issued), so after the barrier stage t is readable and
+    // stage t-1 may be refilled. A fenced __syncthreads() would also drain the
+    // copies still in flight for the later k-tiles.
+    __builtin_amdgcn_s_barrier();
+    if (t + S - 1 < nk) issue(t + S - 1);
+    const int8_t* st = lds + (t % S) * STAGE;
+    v4i af[2][FM], bf[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[0][i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (khalf ^ asw[i]));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      bf[0][j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (khalf ^ bsw[j]));
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KS) {
+        const int c = 2 * (ks + 1) + khalf;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          af[cur ^ 1][i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (c ^ asw[i]));
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          bf[cur ^ 1][j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (c ^ bsw[j]));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  const int col = lane & 31;
+  const int rq = (lane >> 5) * 4;
+  constexpr int KIND = EPI & 15;
+  constexpr int ODT = EPI >> 4;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + j * 32 + col;
+    if (n >= N) continue;
+    float sw = 0.0f, bias = 0.0f;
+    if (KIND == EPI_DEQUANT) {
+      sw = ep.sw[n];
+      if (ep.bias != nullptr) bias = ep.bias[n];
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + rq + (r & 3);
+        if (m >= M) continue;
+        const int32_t v = acc[i][j][r];
+        const int64_t idx = (int64_t)m * N + n;
+        if (KIND == EPI_I32) {
+          Cout[idx] = v;
+        } else if (KIND == EPI_PARTIAL) {
+          ep.partial[(int64_t)blockIdx.z * M * N + idx] = v;
+        } else {
+          float o = (float)v * (ep.sx[m] * sw);
+          if (ep.bias != nullptr) o = o + bias;
+          store_out<ODT>(ep.out, idx, o);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny kernel (M <= 16*MF): each wavefront owns 16 output columns and one
+// K range; fragments are loaded straight from global memory.
+// Requires K % 64 == 0 and every split range a multiple of 64.
+// ---------------------------------------------------------------------------
+template <int MF, int EPI>
+__global__ __launch_bounds__(256) void gemm_skinny(const int8_t* __restrict__ A,
+                                                   const int8_t* __restrict__ B, int M, int N,
+                                                   int K, int k_split, int32_t* __restrict__ C,
+                                                   EpiArgs ep) {
+  constexpr int UNROLL = 4;
+  const int lane = threadIdx.x & 63;
+  const int nb = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = nb * 16 + (lane & 15);
+  const int kofs = (lane >> 4) * 16;
+  const int kb = blockIdx.y * k_split;
+  const int ke = min(kb + k_split, K);
+  if (nb * 16 >= N) return;
+  const int8_t* brow = B + (int64_t)(n < N ? n : 0) * K + kofs;
+  const int8_t* arow[MF];
+  bool aok[MF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+    const int m = i * 16 + (lane & 15);
+    aok[i] = m < M;
+    arow[i] = A + (int64_t)(aok[i] ? m : 0) * K + kofs;
+  }
+  const bool bok = n < N;
+  v4i acc[MF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i) acc[i] = v4i{0, 0, 0, 0};
+  int k0 = kb;
+  for (; k0 + 64 * UNROLL <= ke; k0 += 64 * UNROLL) {
+    v4i bf[UNROLL], af[UNROLL][MF];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      bf[u] = bok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(brow + k0 + 64 * u))
+                  : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+        af[u][i] = aok[i] ? *reinterpret_cast<const v4i*>(arow[i] + k0 + 64 * u) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+        acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[u][i], bf[u], acc[i], 0, 0, 0);
+  }
+  for (; k0 < ke; k0 += 64) {
+    const v4i bf = bok ? *reinterpret_cast<const v4i*>(brow + k0) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const v4i af = aok[i] ? *reinterpret_cast<const v4i*>(arow[i] + k0) : v4i{0, 0, 0, 0};
+      acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, acc[i], 0, 0, 0);
+    }
+  }
+  if (!bok) return;
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = i * 16 + (lane >> 4) * 4 + r;
+      if (m < M) epi_store<EPI>(ep, C, M, N, m, n, acc[i][r], blockIdx.y);
     }
   }
 }
@@ -195,7 +523,7 @@ __global__ __launch_bounds__(256) void gemm_finalize(const int32_t* __restrict__
   }
 }
 
-// Any-shape fallback (K or N not a multiple of 16): one thread per output.
+// Any-shape fallback (K not a multiple of 16): one thread per output.
 __global__ __launch_bounds__(256) void gemm_i8_scalar(const int8_t* __restrict__ A,
                                                      const int8_t* __restrict__ B, int64_t M,
                                                      int64_t N, int64_t K, int32_t* __restrict__ C,
@@ -206,7 +534,7 @@ __global__ __launch_bounds__(256) void gemm_i8_scalar(const int8_t* __restrict__
     const int64_t m = i / N;
     const int64_t n = i - m * N;
     int32_t acc = 0;
-    for (int64_t k = 0; k < K; ++k) acc += (int32_t)A[m * K + k] * (int32_t)B[k * N + n];
+    for (int64_t k = 0; k < K; ++k) acc += (int32_t)A[m * K + k] * (int32_t)B[n * K + k];
     if (!dequant) {
       C[i] = acc;
     } else {
@@ -215,31 +543,88 @@ __global__ __launch_bounds__(256) void gemm_i8_scalar(const int8_t* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// Launch plans
+// ---------------------------------------------------------------------------
+enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_256x256 = 2, K_TILE_128x128 = 3, K_TILE_128x256 = 4,
+            K_TILE_64x128 = 5, K_DMA_256x256 = 6, K_DMA_128x256 = 7, K_DMA_128x128 = 8,
+            K_DMA_256x128 = 9 };
+
 struct Plan {
-  int kind;     // 0 scalar, 1: BM16, 2: BM64, 3: BM128
+  int kind;
+  int mf;       // skinny: 16-row fragments
   int splits;
-  int64_t k_split;
+  int k_split;  // k per split (multiple of the kernel's k step)
+  int bm, bn, bk;
 };
 
+// Tile choice override for tuning sweeps: SI_GEMM_TILE=<Kind> in the
+// environment (read once); unset = automatic choice by M.
+int forced_kind() {
+  static const int kind = [] {
+    const char* v = getenv("SI_GEMM_TILE");
+    return v != nullptr ? atoi(v) : -1;
+  }();
+  return kind;
+}
+
 Plan choose(int64_t M, int64_t N, int64_t K) {
-  Plan p{0, 1, K};
-  if (K % 16 != 0 || N % 16 != 0 || M == 0) return p;
-  int bm;
-  if (M <= 16) { p.kind = 1; bm = 16; }
-  else if (M <= 256) { p.kind = 2; bm = 64; }
-  else { p.kind = 3; bm = 128; }
-  const int64_t tiles = ceil_div(M, bm) * ceil_div(N, 128);
-  const int64_t kt = ceil_div(K, BK);  // k tiles
-  // Split K while the tile grid is small, each split keeps >= 4 k tiles, and
-  // the partial sums (written and re-read, 8 bytes per output per split) stay
-  // within a small fraction of the K*N weight bytes.
-  int splits = 1;
-  while (tiles * splits < 512 && splits < 8 && kt / (splits * 2) >= 4 &&
-         (int64_t)(splits * 2) * M * 16 <= K)
-    splits *= 2;
-  p.splits = splits;
-  p.k_split = ceil_div(kt, splits) * BK;
-  p.splits = (int)ceil_div(K, p.k_split);
+  Plan p{K_SCALAR, 0, 1, (int)K, 0, 0, 0};
+  const bool big = M >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 31);
+  if (K % 16 != 0 || M == 0 || N == 0 || big) return p;
+  int kind;
+  if (forced_kind() >= 0) {
+    kind = forced_kind();
+  } else if (M <= 16 && K % 64 == 0) {
+    kind = K_SKINNY;  // 4096 x 11008, M = 16: 22 us (DMA 128x128: 23 us)
+  } else if (M <= 384 && K % 128 == 0) {
+    kind = K_DMA_128x128;  // M = 64: 24 us, M = 256: 27 us
+  } else if (M <= 768 && K % 64 == 0) {
+    kind = K_DMA_256x128;  // M = 512: 44 us
+  } else if (K % 64 == 0) {
+    kind = K_DMA_256x256;  // M = 1024: 75 us
+  } else {
+    kind = K_TILE_128x128;
+  }
+  if (kind == K_SKINNY) {
+    if (M > 64 || K % 64 != 0) kind = K_TILE_128x128;
+  }
+  p.kind = kind;
+  if (kind == K_SKINNY) {
+    p.mf = (int)ceil_div(M, 16);
+    const int64_t waves = ceil_div(N, 16);
+    const int64_t ksteps = K / 64;
+    int splits = 1;
+    // enough wavefronts to stream the weight (~8 per SIMD), >= 8 k steps each
+    while (waves * splits < 8192 && ksteps / (splits * 2) >= 8) splits *= 2;
+    p.splits = splits;
+    p.k_split = (int)(ceil_div(ksteps, splits) * 64);
+    p.splits = (int)ceil_div(K, p.k_split);
+    return p;
+  }
+  switch (kind) {
+    case K_DMA_256x256: p.bm = 256; p.bn = 256; p.bk = 64; break;
+    case K_DMA_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
+    case K_DMA_256x128: p.bm = 256; p.bn = 128; p.bk = 64; break;
+    case K_DMA_128x128: p.bm = 128; p.bn = 128; p.bk = 128; break;
+    case K_TILE_256x256: p.bm = 256; p.bn = 256; p.bk = 64; break;
+    case K_TILE_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
+    case K_TILE_64x128: p.bm = 64; p.bn = 128; p.bk = 128; break;
+    default: p.bm = 128; p.bn = 128; p.bk = 128; break;
+  }
+  if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0) {  // same tile family, k step 64
+    p.kind = p.kind == K_DMA_128x128 ? K_DMA_256x128 : K_TILE_128x256;
+    p.bm = p.kind == K_DMA_256x128 ? 256 : 128;
+    p.bn = p.kind == K_DMA_256x128 ? 128 : 256;
+    p.bk = 64;
+  }
+  if (K % p.bk != 0) {  // fall back to a k step that divides K
+    p.kind = K_TILE_128x128;
+    p.bm = 128; p.bn = 128; p.bk = 32;
+    if (K % 32 != 0) { p.kind = K_SCALAR; return p; }
+  }
+  p.splits = 1;
+  p.k_split = (int)K;
   return p;
 }
 
@@ -249,24 +634,53 @@ size_t workspace_for(int64_t M, int64_t N, int64_t K) {
 }
 
 template <int EPI>
-void launch_tiles(const Plan& p, const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K,
-                  int32_t* c, const EpiArgs& ep, hipStream_t st) {
-  dim3 block(256);
-  switch (p.kind) {
-    case 1: {
-      dim3 grid((unsigned)ceil_div(N, 128), (unsigned)ceil_div(M, 16), (unsigned)p.splits);
-      gemm_i8_mfma<16, 128, 1, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-      break;
+void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
+                 const EpiArgs& ep, hipStream_t st) {
+  const dim3 block(256);
+  const dim3 grid((unsigned)ceil_div(N, p.bn), (unsigned)ceil_div(M, p.bm), (unsigned)p.splits);
+  if (p.kind == K_DMA_256x256) {
+    gemm_dma<256, 256, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_DMA_128x256) {
+    gemm_dma<128, 256, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_DMA_256x128) {
+    gemm_dma<256, 128, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_DMA_128x128) {
+    gemm_dma<128, 128, 128, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_TILE_256x256) {
+    gemm_tile<256, 256, 64, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_TILE_128x256) {
+    gemm_tile<128, 256, 64, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.kind == K_TILE_64x128) {
+    gemm_tile<64, 128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else if (p.bk == 32) {
+    gemm_tile<128, 128, 32, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  } else {
+    gemm_tile<128, 128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  }
+}
+
+template <int EPI>
+void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
+            const EpiArgs& ep, hipStream_t st) {
+  const dim3 block(256);
+  if (p.kind == K_SKINNY) {
+    const dim3 grid((unsigned)ceil_div(ceil_div(N, 16), 4), (unsigned)p.splits);
+    switch (p.mf) {
+      case 1: gemm_skinny<1, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep); break;
+      case 2: gemm_skinny<2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep); break;
+      case 3: gemm_skinny<3, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep); break;
+      default: gemm_skinny<4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
     }
-    case 2: {
-      dim3 grid((unsigned)ceil_div(N, 128), (unsigned)ceil_div(M, 64), (unsigned)p.splits);
-      gemm_i8_mfma<64, 128, 1, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-      break;
-    }
-    default: {
-      dim3 grid((unsigned)ceil_div(N, 128), (unsigned)ceil_div(M, 128), (unsigned)p.splits);
-      gemm_i8_mfma<128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-    }
+    return;
+  }
+  if (EPI != EPI_DEQUANT) {
+    launch_tile<EPI>(p, a, b, M, N, K, c, ep, st);
+  } else if (ep.out_dtype == SI_DT_F32) {
+    launch_tile<EPI_DEQUANT + 16 * SI_DT_F32>(p, a, b, M, N, K, c, ep, st);
+  } else if (ep.out_dtype == SI_DT_F16) {
+    launch_tile<EPI_DEQUANT + 16 * SI_DT_F16>(p, a, b, M, N, K, c, ep, st);
+  } else {
+    launch_tile<EPI_DEQUANT + 16 * SI_DT_BF16>(p, a, b, M, N, K, c, ep, st);
   }
 }
 
@@ -274,15 +688,19 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
              EpiArgs ep, bool dequant, void* ws, size_t ws_bytes, hipStream_t st, const char* who) {
   if (M == 0 || N == 0) return SI_OK;
   const Plan p = choose(M, N, K);
-  if (p.kind == 0) {
-    const int64_t total = M * N;
-    const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 65536);
+  if (p.kind == K_SCALAR) {
+    const int64_t blocks = std::min<int64_t>(ceil_div(M * N, 256), 65536);
     gemm_i8_scalar<<<(unsigned)blocks, 256, 0, st>>>(a, b, M, N, K, c, ep, dequant ? 1 : 0);
     return check_launch(who);
   }
+  if (ceil_div(M, p.bm > 0 ? p.bm : 1) >= 65536 || p.splits >= 65536) {
+    set_error("%s: shape too large", who);
+    return SI_ERR_INVALID;
+  }
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
   if (p.splits == 1) {
-    if (dequant) launch_tiles<EPI_DEQUANT>(p, a, b, M, N, K, c, ep, st);
-    else launch_tiles<EPI_I32>(p, a, b, M, N, K, c, ep, st);
+    if (dequant) launch<EPI_DEQUANT>(p, a, b, Mi, Ni, Ki, c, ep, st);
+    else launch<EPI_I32>(p, a, b, Mi, Ni, Ki, c, ep, st);
     return check_launch(who);
   }
   const size_t need = workspace_for(M, N, K);
@@ -291,7 +709,7 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
     return SI_ERR_INVALID;
   }
   ep.partial = reinterpret_cast<int32_t*>(ws);
-  launch_tiles<EPI_PARTIAL>(p, a, b, M, N, K, c, ep, st);
+  launch<EPI_PARTIAL>(p, a, b, Mi, Ni, Ki, c, ep, st);
   if (int rc = check_launch(who)) return rc;
   const int64_t blocks = std::min<int64_t>(ceil_div(M * N, 256), 65536);
   gemm_finalize<<<(unsigned)blocks, 256, 0, st>>>(ep.partial, p.splits, M, N, c, ep,
@@ -316,6 +734,8 @@ extern "C" int si_gemm_i8i8_i32(const int8_t* a, const int8_t* b, int64_t M, int
   SI_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "si_gemm_i8i8_i32: bad shape");
   if (M == 0 || N == 0) return SI_OK;
   SI_CHECK_ARG(a && b && c, "si_gemm_i8i8_i32: NULL argument");
+  SI_CHECK_ARG(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0,
+               "si_gemm_i8i8_i32: operands must be 16-byte aligned");
   EpiArgs ep{nullptr, nullptr, nullptr, nullptr, 0, nullptr};
   return run_gemm(a, b, M, N, K, c, ep, false, workspace, workspace_bytes, as_stream(stream),
                   "si_gemm_i8i8_i32");
@@ -330,6 +750,8 @@ extern "C" int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t
   SI_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "si_gemm_i8_dequant: bad shape");
   if (M == 0 || N == 0) return SI_OK;
   SI_CHECK_ARG(a && sx && b && sw && out, "si_gemm_i8_dequant: NULL argument");
+  SI_CHECK_ARG(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0,
+               "si_gemm_i8_dequant: operands must be 16-byte aligned");
   EpiArgs ep{sx, sw, bias, out, out_dtype, nullptr};
   return run_gemm(a, b, M, N, K, nullptr, ep, true, workspace, workspace_bytes,
                   as_stream(stream), "si_gemm_i8_dequant");

@@ -162,34 +162,17 @@ __global__ __launch_bounds__(256) void weight_scale_kernel(const float* __restri
   }
 }
 
-// Step 2: q = clamp(rint(w / s), -127, 127), written transposed to [K, N]
-// through a 64x64 LDS tile so both the read of w and the write of qT are
-// coalesced.
+// Step 2: q = clamp(rint(w / s), -127, 127) in the [N, K] layout of w.
 __global__ __launch_bounds__(256) void weight_quant_kernel(const float* __restrict__ w, int64_t N,
                                                            int64_t K,
                                                            const float* __restrict__ scale,
-                                                           int8_t* __restrict__ qT) {
-  __shared__ int8_t tile[64][65];
-  const int64_t n0 = (int64_t)blockIdx.y * 64;
-  const int64_t k0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63;
-  const int ty = threadIdx.x >> 6;  // 0..3
-  for (int i = ty; i < 64; i += 4) {
-    const int64_t n = n0 + i;
-    const int64_t k = k0 + tx;
-    int8_t v = 0;
-    if (n < N && k < K) {
-      float r = rintf(w[n * K + k] / scale[n]);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      v = (int8_t)(int)r;
-    }
-    tile[i][tx] = v;  // tile[n][k]
-  }
-  __syncthreads();
-  for (int i = ty; i < 64; i += 4) {
-    const int64_t k = k0 + i;
-    const int64_t n = n0 + tx;
-    if (n < N && k < K) qT[k * N + n] = tile[tx][i];
+                                                           int8_t* __restrict__ q) {
+  const int64_t total = N * K;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float r = rintf(w[i] / scale[i / K]);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    q[i] = (int8_t)(int)r;
   }
 }
 
@@ -279,11 +262,9 @@ extern "C" int si_weight_quant_i8(const float* w, int64_t N, int64_t K, int8_t* 
   clear_error();
   SI_CHECK_ARG(N > 0 && K > 0, "si_weight_quant_i8: bad shape");
   SI_CHECK_ARG(w && qweight && scale, "si_weight_quant_i8: NULL argument");
-  SI_CHECK_ARG(ceil_div(N, 64) < 65536, "si_weight_quant_i8: N too large");
   hipStream_t st = as_stream(stream);
   weight_scale_kernel<<<(unsigned)(N < 65536 ? N : 65536), 256, 0, st>>>(w, N, K, scale);
   if (int rc = check_launch("si_weight_quant_i8/scale")) return rc;
-  dim3 grid((unsigned)ceil_div(K, 64), (unsigned)ceil_div(N, 64));
-  weight_quant_kernel<<<grid, 256, 0, st>>>(w, N, K, scale, qweight);
+  weight_quant_kernel<<<grid_for(N * K, 256), 256, 0, st>>>(w, N, K, scale, qweight);
   return check_launch("si_weight_quant_i8/quant");
 }

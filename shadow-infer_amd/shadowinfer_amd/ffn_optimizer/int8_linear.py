@@ -2,7 +2,11 @@
 (shadowinfer/ffn_optimizer/int8_linear.py:25-216) on a gfx950 MFMA GEMM.
 
 Weights: symmetric per output channel, ``s_w = max(amax_k|w| / 127, 1e-8)``,
-``q_w = clamp(round(w / s_w), -127, 127)``, stored transposed ``[K, N]``.
+``q_w = clamp(round(w / s_w), -127, 127)``. The device buffer keeps
+nn.Linear's ``[N, K]`` layout (K contiguous: the MFMA fragment layout, so the
+GEMM streams it without transposition); ``qweight`` is the reference's
+``[K, N]`` tensor as a view of it, and the state dict reads and writes the
+reference's ``qweight [K, N]`` key.
 Activations: per token row, ``s_x = max(amax / 127, 1e-8)``,
 ``q_x = clamp(round(x / s_x), -127, 127)``. The int8 x int8 -> int32 product
 runs on MFMA (exact), then ``out = T(float(acc) * (s_x * s_w) [+ bias])``.
@@ -32,8 +36,11 @@ class INT8Linear(nn.Module):
 
     def __init__(self, qweight: torch.Tensor, weight_scale: torch.Tensor,
                  bias: Optional[torch.Tensor] = None, in_features: Optional[int] = None,
-                 out_features: Optional[int] = None) -> None:
+                 out_features: Optional[int] = None, *,
+                 _qweight_nk: Optional[torch.Tensor] = None) -> None:
         super().__init__()
+        if _qweight_nk is not None:
+            qweight = _qweight_nk.t()
         if qweight.dim() != 2:
             raise ValueError(f"qweight must be 2-D, got shape {tuple(qweight.shape)}")
         if qweight.dtype != torch.int8:
@@ -50,7 +57,8 @@ class INT8Linear(nn.Module):
             raise ValueError(f"bias must have {out_features} elements")
         self.in_features = int(in_features)
         self.out_features = int(out_features)
-        self.register_buffer("qweight", qweight.to(torch.int8).contiguous())
+        nk = _qweight_nk if _qweight_nk is not None else qweight.t()
+        self.register_buffer("qweight_nk", nk.to(torch.int8).contiguous())
         self.register_buffer("weight_scale", weight_scale.to(torch.float32).contiguous())
         if bias is None:
             self.register_buffer("bias", None)
@@ -65,13 +73,31 @@ class INT8Linear(nn.Module):
         weight = linear.weight.detach().to(torch.float32).contiguous()
         _native.require_device(weight, "INT8Linear.from_linear")
         N, K = weight.shape
-        qweight = torch.empty((K, N), dtype=torch.int8, device=weight.device)
+        q_nk = torch.empty((N, K), dtype=torch.int8, device=weight.device)
         scale = torch.empty(N, dtype=torch.float32, device=weight.device)
-        _native.call("si_weight_quant_i8", weight.data_ptr(), N, K, qweight.data_ptr(),
+        _native.call("si_weight_quant_i8", weight.data_ptr(), N, K, q_nk.data_ptr(),
                      scale.data_ptr(), _native.stream(weight.device))
         bias = None if linear.bias is None else linear.bias.detach().to(torch.float32).clone()
-        return cls(qweight=qweight, weight_scale=scale, bias=bias,
-                   in_features=linear.in_features, out_features=linear.out_features)
+        return cls(qweight=None, weight_scale=scale, bias=bias, in_features=linear.in_features,
+                   out_features=linear.out_features, _qweight_nk=q_nk)
+
+    @property
+    def qweight(self) -> torch.Tensor:
+        """The reference's ``[in_features, out_features]`` int8 weight (a view)."""
+        return self.qweight_nk.t()
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        w = destination.pop(prefix + "qweight_nk")
+        destination[prefix + "qweight"] = w.t() if keep_vars else w.t().contiguous()
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        key = prefix + "qweight"
+        if key in state_dict:
+            state_dict[prefix + "qweight_nk"] = state_dict.pop(key).t().contiguous()
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
 
     @property
     def using_int_mm(self) -> bool:
@@ -91,8 +117,8 @@ class INT8Linear(nn.Module):
         if flat.numel() == 0:
             return torch.empty((*leading_shape, self.out_features), dtype=x.dtype, device=x.device)
         _native.require_device(flat, "INT8Linear.forward")
-        if self.qweight.device != flat.device:
-            raise ValueError(f"input on {flat.device} but weights on {self.qweight.device}")
+        if self.qweight_nk.device != flat.device:
+            raise ValueError(f"input on {flat.device} but weights on {self.qweight_nk.device}")
         dt = _native.dtype_code(flat.dtype)
         flat = flat.contiguous()
         M, K, N = flat.shape[0], self.in_features, self.out_features
@@ -100,7 +126,7 @@ class INT8Linear(nn.Module):
         ws_bytes = _native.size_query("si_int8_linear_workspace_bytes", M, K, N)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
         _native.call("si_int8_linear_forward", flat.data_ptr(), dt, M, K, N,
-                     self.qweight.data_ptr(), self.weight_scale.data_ptr(),
+                     self.qweight_nk.data_ptr(), self.weight_scale.data_ptr(),
                      _native.ptr(self.bias), out.data_ptr(), ws.data_ptr(), ws_bytes,
                      _native.stream(x.device))
         return out.reshape(*leading_shape, N)

@@ -20,10 +20,12 @@ from shadowinfer_amd.utils import Quantizer
 pytestmark = pytest.mark.gpu
 
 
-def _gemm_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """si_gemm_i8i8_i32 through the C ABI."""
+def _gemm_i32(a: torch.Tensor, b_kn: torch.Tensor) -> torch.Tensor:
+    """si_gemm_i8i8_i32 through the C ABI; ``b_kn`` is the reference's [K, N]
+    operand, passed to the library in its [N, K] layout."""
     M, K = a.shape
-    N = b.shape[1]
+    N = b_kn.shape[1]
+    b = b_kn.t().contiguous()
     c = torch.empty(M, N, dtype=torch.int32, device=a.device)
     ws_bytes = _native.size_query("si_gemm_workspace_bytes", M, N, K)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=a.device)
@@ -49,7 +51,8 @@ def _exact_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 @pytest.mark.parametrize("M,K,N", [(1, 64, 16), (5, 128, 96), (16, 4096, 11008),
                                    (64, 4096, 11008), (33, 256, 48), (300, 512, 272),
-                                   (7, 40, 24), (3, 17, 5)])
+                                   (7, 40, 24), (3, 17, 5), (100, 96, 48), (65, 4096, 200),
+                                   (900, 1024, 300), (17, 11008, 4096)])
 def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
     g = torch.Generator().manual_seed(M * 7 + K + N)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
@@ -183,6 +186,24 @@ def test_extreme_inputs_finite(dev, kind):
          "large": torch.randn(4, 128) * 1e4}[kind].to(dev)
     out = layer(x)
     assert bool(torch.isfinite(out).all())
+
+
+def test_state_dict_uses_reference_layout(dev):
+    """The state dict holds the reference's qweight [K, N]; loading it (or a
+    reference-made state dict) restores the same layer."""
+    torch.manual_seed(4)
+    layer = INT8Linear.from_linear(nn.Linear(128, 96, bias=True).to(dev))
+    sd = layer.state_dict()
+    assert set(sd) == {"qweight", "weight_scale", "bias"}
+    assert sd["qweight"].shape == (128, 96) and sd["qweight"].is_contiguous()
+    fresh = INT8Linear(torch.zeros(128, 96, dtype=torch.int8, device=dev),
+                       torch.ones(96, device=dev), bias=torch.zeros(96, device=dev))
+    fresh.load_state_dict(sd)
+    assert torch.equal(fresh.qweight, layer.qweight)
+    x = torch.randn(8, 128, device=dev)
+    assert torch.equal(fresh(x), layer(x))
+    built = INT8Linear(sd["qweight"], sd["weight_scale"], sd["bias"])
+    assert torch.equal(built(x), layer(x))
 
 
 def test_empty_invalid_and_memory(dev):
