@@ -15,7 +15,8 @@ dominant kernel, the INT8 FFN GEMM (4096 x 11008, M in {16, 64, 256, 1024}) in
 TOPS against the int8 MFMA peak, the fused packed-KV attention, and the CPU
 baseline (the oracle on the host, a bounded sample of the same workload).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--part all|kv|gemm|attention|calib]
 """
 
 from __future__ import annotations
@@ -35,6 +36,7 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16/bf16 MFMA, TFLOP/s
 
 LAYERS, B, S, H, D = 32, 1, 8192, 32, 128
 GROUP = 16
+CALIB_BYTES = 512 << 20
 
 
 def log(msg: str) -> None:
@@ -304,16 +306,35 @@ def cpu_baseline(layers: int = 4):
             "seconds": total_s}
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the factor a plain
+    copy of known size gives); None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "kv_7b_layer_hbm_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--quick", action="store_true", help="skip GEMM and attention extras")
-    ap.add_argument("--calib", action="store_true",
-                    help="also run a plain 512 MiB device copy (counter calibration)")
+    ap.add_argument("--quick", action="store_true", help="same as --part kv")
+    ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "calib"), default="all",
+                    help="run one part only (for profiling); 'calib' runs the plain device "
+                         "fill and copy that calibrate the HBM byte counters")
     args = ap.parse_args()
+    if args.quick:
+        args.part = "kv"
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -326,19 +347,26 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(dev)}")
 
-    if args.calib:
-        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    if args.part == "calib":
+        # Counter calibration: a fill (writes CALIB_BYTES) and device-to-device
+        # copies (read CALIB_BYTES, write CALIB_BYTES), nothing else.
+        src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log("calibration copy: 3 x 512 MiB device-to-device")
-        del src, dst
+        print(json.dumps({"calibration": "fill + 3 copies", "bytes": CALIB_BYTES}), flush=True)
+        return
+    if args.part in ("gemm", "attention"):
+        fn = bench_gemm if args.part == "gemm" else bench_attention
+        log(args.part)
+        print(json.dumps({args.part: fn(torch, dev)}), flush=True)
+        return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
     log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
     gemm = attn = None
-    if not args.quick:
+    if args.part == "all":
         log("int8 gemm")
         gemm = bench_gemm(torch, dev)
         log("attention")
@@ -377,7 +405,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(f"kv_{dom}"),
             "bytes_per_launch": int(kv[f"{dom}_bytes_per_launch"]),
             "avg_launch_us": round(kv[f"{dom}_us"], 3),
         },
