@@ -45,6 +45,7 @@ struct EpiArgs {
   void* out;
   int out_dtype;
   int32_t* partial;  // [splits, M, N] when EPI_PARTIAL
+  int vec;           // 16-byte stores allowed: N % 8 == 0 and every output/scale pointer aligned
 };
 
 // out = T(float(acc) * (sx * sw) [+ bias]) with the reference's rounding order.
@@ -254,11 +255,24 @@ __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
 
 // ---------------------------------------------------------------------------
 // DMA tile kernel: global -> LDS copies by global_load_lds_dwordx4 (no register
-// staging), S LDS stages, so k-tiles t+1 .. t+S-2 are in flight while the
+// staging) into S LDS stages, so k-tiles t+1 .. t+S-2 are in flight while the
 // MFMAs of k-tile t run. One wave instruction fills 1 KB of LDS, lane l the
 // 16 bytes at 16*l: rows of a stage are therefore unpadded (BK bytes) and the
 // 16-byte chunks of row r are stored at slot chunk ^ swz(r); swz spreads the
-// rows read by one fragment load over distinct banks (32- and 64-bank LDS).
+// rows read by one fragment load over distinct banks.
+//
+// MFMA fragments are double-buffered in registers: the loads for k-slice s+1
+// are issued between the MFMAs of k-slice s, and the first k-slice of k-tile
+// t+1 is loaded during the last k-slice of k-tile t (after the one barrier per
+// k-tile), so LDS latency stays behind the MFMA pipe. sched_group_barrier
+// pins that interleave (the scheduler would otherwise sink every load next to
+// its first use to save registers).
+//
+// Epilogue: the accumulators of each 32-row fragment row go through the wave's
+// own LDS staging area, then every lane handles 8 consecutive outputs of one
+// row: int32 as two 16-byte stores, dequantized values with one scale load per
+// row and 16-byte stores of the output type.
+//
 // Requires K % BK == 0 (K per split too) and 16-byte aligned operands.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(1))) void gvoid_t;
@@ -270,37 +284,85 @@ __device__ __forceinline__ int chunk_swz(int r) {
   else return (r ^ (r >> 1)) & 7;
 }
 
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+// s_waitcnt vmcnt(VM) lgkmcnt(LGKM), expcnt left alone (gfx9 encoding).
+template <int VM, int LGKM = 15>
+__device__ __forceinline__ void wait_cnt() {
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "counter range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (LGKM << 8));
+}
+
+// Wait until at most n k-tiles of this wave's copies are still in flight
+// (n <= S - 2 <= 2), with every LDS read of this wave complete.
+template <int LPT, int S>
+__device__ __forceinline__ void wait_tiles(int n) {
+  static_assert(S >= 2 && S <= 4, "stage count");
+  if (S == 4 && n >= 2) wait_cnt<(S == 4 ? 2 * LPT : 0), 0>();
+  else if (S >= 3 && n >= 1) wait_cnt<(S >= 3 ? LPT : 0), 0>();
+  else wait_cnt<0, 0>();
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs. Renumber them so
+// that each XCD receives a contiguous run of tile ids: with M-tiles fastest,
+// the tiles that read the same weight columns then share one L2.
+__device__ __forceinline__ int xcd_order(int b, int n) {
+  constexpr int X = 8;
+  const int per = (n + X - 1) / X;     // tiles on each of the first `tall` XCDs
+  const int tall = n - (per - 1) * X;  // 1..8
+  const int x = b % X, j = b / X;
+  return x < tall ? x * per + j : tall * per + (x - tall) * (per - 1) + j;
+}
+
+template <int ODT>
+__device__ __forceinline__ void store8(void* out, int64_t idx, const float* o) {
+  if constexpr (ODT == SI_DT_F32) {
+    float* p = reinterpret_cast<float*>(out) + idx;
+    reinterpret_cast<float4*>(p)[0] = make_float4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(o[4], o[5], o[6], o[7]);
+  } else {
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = ODT == SI_DT_F16 ? f32_to_f16_bits(o[e]) : f32_to_bf16_bits(o[e]);
+    v4i w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = (int)(h[2 * e] | (h[2 * e + 1] << 16));
+    *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(out) + idx) = w;
+  }
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int S, int EPI>
-__global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
-                                                const int8_t* __restrict__ B, int M, int N, int K,
-                                                int k_split, int32_t* __restrict__ Cout,
-                                                EpiArgs ep) {
-  static_assert(WM * WN == 4, "four waves per block");
+__global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restrict__ A,
+                                                         const int8_t* __restrict__ B, int M,
+                                                         int N, int K, int k_split,
+                                                         int32_t* __restrict__ Cout, EpiArgs ep) {
+  constexpr int NW = WM * WN;  // 4 waves (one per SIMD) or 8 (two per SIMD)
+  static_assert(NW == 4 || NW == 8, "four or eight waves per block");
   constexpr int CPR = BK / 16;
-  constexpr int LA = BM * BK / 1024 / 4;  // 1-KB DMA blocks of A per wave per k-tile
-  constexpr int LB = BN * BK / 1024 / 4;
-  static_assert(LA * 4096 == BM * BK && LB * 4096 == BN * BK, "whole DMA blocks per wave");
-  constexpr int LPT = LA + LB;            // vm loads per thread per k-tile
+  constexpr int LA = BM * BK / 1024 / NW;  // 1-KB DMA blocks of A per wave per k-tile
+  constexpr int LB = BN * BK / 1024 / NW;
+  static_assert(LA * 1024 * NW == BM * BK && LB * 1024 * NW == BN * BK, "whole DMA blocks per wave");
+  constexpr int LPT = LA + LB;        // vm loads per thread per k-tile
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
+  static_assert(FM * 32 == TM && FN * 32 == TN, "32-row fragments");
   constexpr int KS = BK / 32;
+  static_assert(KS % 2 == 0, "fragment buffers alternate per k-slice");
+  constexpr int EP = TN + 8;  // epilogue staging pitch in words (rows r and r+4 on other banks)
+  static_assert(NW * 16 * EP * 4 <= S * STAGE, "epilogue staging fits in the stages");
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave / WN;
   const int wn = wave % WN;
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * BN;
-  const int kb = blockIdx.z * k_split;
+  const int ntiles = (int)gridDim.x;
+  const int g = xcd_order((int)(blockIdx.x + blockIdx.z * gridDim.x), ntiles * (int)gridDim.z);
+  const int tile = g % ntiles;
+  const int split = g / ntiles;
+  const int nM = (M + BM - 1) / BM;
+  const int m0 = (tile % nM) * BM;
+  const int n0 = (tile / nM) * BN;
+  const int kb = split * k_split;
   const int ke = min(kb + k_split, K);
   const int nk = (ke - kb) / BK;
 
@@ -309,7 +371,7 @@ __global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
   const int8_t* bsrc[LB];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int p = (i * 4 + wave) * 1024 + 16 * lane;
+    const int p = (i * NW + wave) * 1024 + 16 * lane;
     const int r = p / BK;
     const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
     const int m = min(m0 + r, M - 1);  // rows past M feed only discarded outputs
@@ -317,7 +379,7 @@ __global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
   }
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
-    const int p = (i * 4 + wave) * 1024 + 16 * lane;
+    const int p = (i * NW + wave) * 1024 + 16 * lane;
     const int r = p / BK;
     const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
     const int n = min(n0 + r, N - 1);
@@ -329,11 +391,11 @@ __global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
 #pragma unroll
     for (int i = 0; i < LA; ++i)
       __builtin_amdgcn_global_load_lds((gvoid_t*)(asrc[i] + k0),
-                                       (lvoid_t*)(st + (i * 4 + wave) * 1024), 16, 0, 0);
+                                       (lvoid_t*)(st + (i * NW + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < LB; ++i)
       __builtin_amdgcn_global_load_lds((gvoid_t*)(bsrc[i] + k0),
-                                       (lvoid_t*)(st + BM * BK + (i * 4 + wave) * 1024), 16, 0, 0);
+                                       (lvoid_t*)(st + BM * BK + (i * NW + wave) * 1024), 16, 0, 0);
   };
 
   v16i acc[FM][FN];
@@ -359,79 +421,128 @@ __global__ __launch_bounds__(256) void gemm_dma(const int8_t* __restrict__ A,
     bsw[j] = chunk_swz<CPR>(r);
   }
   const int khalf = lane >> 5;
+  v4i af[2][FM], bf[2][FN];
+  auto load_frags = [&](const int8_t* st, int ks, v4i* a, v4i* b) {
+    const int c = 2 * ks + khalf;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (c ^ asw[i]));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (c ^ bsw[j]));
+  };
 
-  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
-  for (int t = 0; t < nk; ++t) {
-    const int rem = min(nk - 1 - t, S - 2);
-    if (rem >= S - 2) wait_vmcnt<(S - 2) * LPT>();
-    else if (S > 3 && rem == 1) wait_vmcnt<LPT>();
-    else wait_vmcnt<0>();
-    // Bare barrier: this wave's copies of k-tile t are complete (waited
-    // above) and its LDS reads of k-tile t-1 have returned (the MFMAs that
-    // consumed them were issued), so after the barrier stage t is readable and
-    // stage t-1 may be refilled. A fenced __syncthreads() would also drain the
-    // copies still in flight for the later k-tiles.
+  if (nk > 0) {
+    for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
+    wait_tiles<LPT, S>(min(nk - 1, S - 2));
     __builtin_amdgcn_s_barrier();
+    load_frags(lds, 0, af[0], bf[0]);
+  }
+  for (int t = 0; t < nk; ++t) {
+    // Stage (t-1) % S is free: every wave passed the barrier of k-tile t-1's
+    // last k-slice after its reads of k-tile t-1 had completed.
     if (t + S - 1 < nk) issue(t + S - 1);
     const int8_t* st = lds + (t % S) * STAGE;
-    v4i af[2][FM], bf[2][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[0][i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (khalf ^ asw[i]));
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      bf[0][j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (khalf ^ bsw[j]));
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int cur = ks & 1;
       if (ks + 1 < KS) {
-        const int c = 2 * (ks + 1) + khalf;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[cur ^ 1][i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (c ^ asw[i]));
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bf[cur ^ 1][j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (c ^ bsw[j]));
+        load_frags(st, ks + 1, af[cur ^ 1], bf[cur ^ 1]);
+      } else {
+        // k-tile t+1: this wave's copies have landed and its reads of k-tile
+        // t are complete; after the barrier the same holds for every wave.
+        // Unconditional (branch-free, so the loads interleave with the MFMAs
+        // below): after the last k-tile it waits for nothing and reads a
+        // stale stage whose fragments are never used.
+        wait_tiles<LPT, S>(min(nk - 2 - t, S - 2));
+        __builtin_amdgcn_s_barrier();
+        load_frags(lds + ((t + 1) % S) * STAGE, 0, af[cur ^ 1], bf[cur ^ 1]);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
+      // Interleave: one MFMA, one LDS read, ... then the remaining MFMAs.
+      constexpr int NL = FM + FN, NMF = FM * FN, NP = NL < NMF ? NL : NMF;
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if constexpr (NMF > NP) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NP, 0);
+      if constexpr (NL > NP) __builtin_amdgcn_sched_group_barrier(0x100, NL - NP, 0);
     }
   }
 
+  // ------------------------------------------------------------- epilogue
+  __syncthreads();  // every wave is done with the stages
+  // Staging in passes of 16 rows: accumulator registers r in [8h, 8h+8) of a
+  // 32x32 fragment hold rows 16h .. 16h+15 (row 8*(r/4) + 4*(lane/32) + r%4).
+  int32_t* stg = reinterpret_cast<int32_t*>(lds) + wave * (16 * EP);
   const int col = lane & 31;
   const int rq = (lane >> 5) * 4;
   constexpr int KIND = EPI & 15;
   constexpr int ODT = EPI >> 4;
+  constexpr int CH = TN / 8;  // 8-wide chunks per staged row
+  int32_t* dst = KIND == EPI_PARTIAL ? ep.partial + (int64_t)split * M * N : Cout;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * TN + j * 32 + col;
-    if (n >= N) continue;
-    float sw = 0.0f, bias = 0.0f;
-    if (KIND == EPI_DEQUANT) {
-      sw = ep.sw[n];
-      if (ep.bias != nullptr) bias = ep.bias[n];
-    }
+  for (int i = 0; i < FM; ++i) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + rq + (r & 3);
-        if (m >= M) continue;
-        const int32_t v = acc[i][j][r];
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 8 * h; r < 8 * h + 8; ++r)
+          stg[(8 * (r >> 2) - 16 * h + rq + (r & 3)) * EP + j * 32 + col] = acc[i][j][r];
+      wait_cnt<63, 0>();
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int c = lane; c < 16 * CH; c += 64) {
+        const int row = c / CH;
+        const int ch = c % CH;
+        const int m = m0 + wm * TM + i * 32 + 16 * h + row;
+        const int n = n0 + wn * TN + ch * 8;
+        if (m >= M || n >= N) continue;
+        const int32_t* sp = stg + row * EP + ch * 8;
+        const v4i lo = *reinterpret_cast<const v4i*>(sp);
+        const v4i hi = *reinterpret_cast<const v4i*>(sp + 4);
+        const int32_t v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         const int64_t idx = (int64_t)m * N + n;
-        if (KIND == EPI_I32) {
-          Cout[idx] = v;
-        } else if (KIND == EPI_PARTIAL) {
-          ep.partial[(int64_t)blockIdx.z * M * N + idx] = v;
+        const bool full = ep.vec && n + 8 <= N;
+        if constexpr (KIND != EPI_DEQUANT) {
+          if (full) {
+            reinterpret_cast<v4i*>(dst + idx)[0] = lo;
+            reinterpret_cast<v4i*>(dst + idx)[1] = hi;
+          } else {
+            for (int e = 0; e < 8 && n + e < N; ++e) dst[idx + e] = v[e];
+          }
         } else {
-          float o = (float)v * (ep.sx[m] * sw);
-          if (ep.bias != nullptr) o = o + bias;
-          store_out<ODT>(ep.out, idx, o);
+          const float sx = ep.sx[m];
+          float o[8];
+          if (full) {
+            const float4 w0 = reinterpret_cast<const float4*>(ep.sw + n)[0];
+            const float4 w1 = reinterpret_cast<const float4*>(ep.sw + n)[1];
+            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (float)v[e] * (sx * w[e]);
+            if (ep.bias != nullptr) {
+              const float4 b0 = reinterpret_cast<const float4*>(ep.bias + n)[0];
+              const float4 b1 = reinterpret_cast<const float4*>(ep.bias + n)[1];
+              const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+              for (int e = 0; e < 8; ++e) o[e] = o[e] + bb[e];
+            }
+            store8<ODT>(ep.out, idx, o);
+          } else {
+            for (int e = 0; e < 8 && n + e < N; ++e) {
+              float x = (float)v[e] * (sx * ep.sw[n + e]);
+              if (ep.bias != nullptr) x = x + ep.bias[n + e];
+              store_out<ODT>(ep.out, idx + e, x);
+            }
+          }
         }
       }
+      wait_cnt<63, 0>();
+      __builtin_amdgcn_wave_barrier();
     }
   }
 }
@@ -546,9 +657,12 @@ __global__ __launch_bounds__(256) void gemm_i8_scalar(const int8_t* __restrict__
 // ---------------------------------------------------------------------------
 // Launch plans
 // ---------------------------------------------------------------------------
-enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_256x256 = 2, K_TILE_128x128 = 3, K_TILE_128x256 = 4,
-            K_TILE_64x128 = 5, K_DMA_256x256 = 6, K_DMA_128x256 = 7, K_DMA_128x128 = 8,
-            K_DMA_256x128 = 9 };
+enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
+            K_DMA_128x256 = 7, K_DMA_128x128 = 8, K_DMA_256x128 = 9, K_DMA_256x192 = 10,
+            K_DMA_256x64 = 11, K_DMA_256x128_K128 = 12,
+            // eight waves per block (two per SIMD)
+            K_DMA8_256x256 = 13, K_DMA8_256x256_K128 = 14, K_DMA8_256x192_K128 = 15,
+            K_DMA8_256x128 = 16, K_DMA8_128x256 = 17 };
 
 struct Plan {
   int kind;
@@ -578,11 +692,13 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (M <= 16 && K % 64 == 0) {
     kind = K_SKINNY;  // 4096 x 11008, M = 16: 22 us (DMA 128x128: 23 us)
   } else if (M <= 384 && K % 128 == 0) {
-    kind = K_DMA_128x128;  // M = 64: 24 us, M = 256: 27 us
-  } else if (M <= 768 && K % 64 == 0) {
-    kind = K_DMA_256x128;  // M = 512: 44 us
+    kind = K_DMA_128x128;  // M = 64: 21 us, M = 256: 25 us
+  } else if (M <= 640 && K % 128 == 0) {
+    kind = K_DMA_256x128_K128;  // M = 512: 37 us
+  } else if (K % 128 == 0) {
+    kind = K_DMA8_256x192_K128;  // M = 1024: 61 us, M = 2048: 125 us
   } else if (K % 64 == 0) {
-    kind = K_DMA_256x256;  // M = 1024: 75 us
+    kind = K_DMA_256x192;
   } else {
     kind = K_TILE_128x128;
   }
@@ -607,20 +723,23 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     case K_DMA_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
     case K_DMA_256x128: p.bm = 256; p.bn = 128; p.bk = 64; break;
     case K_DMA_128x128: p.bm = 128; p.bn = 128; p.bk = 128; break;
-    case K_TILE_256x256: p.bm = 256; p.bn = 256; p.bk = 64; break;
-    case K_TILE_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
-    case K_TILE_64x128: p.bm = 64; p.bn = 128; p.bk = 128; break;
-    default: p.bm = 128; p.bn = 128; p.bk = 128; break;
+    case K_DMA_256x192: p.bm = 256; p.bn = 192; p.bk = 64; break;
+    case K_DMA_256x64: p.bm = 256; p.bn = 64; p.bk = 128; break;
+    case K_DMA_256x128_K128: p.bm = 256; p.bn = 128; p.bk = 128; break;
+    case K_DMA8_256x256: p.bm = 256; p.bn = 256; p.bk = 64; break;
+    case K_DMA8_256x256_K128: p.bm = 256; p.bn = 256; p.bk = 128; break;
+    case K_DMA8_256x192_K128: p.bm = 256; p.bn = 192; p.bk = 128; break;
+    case K_DMA8_256x128: p.bm = 256; p.bn = 128; p.bk = 64; break;
+    case K_DMA8_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
+    default: p.kind = K_TILE_128x128; p.bm = 128; p.bn = 128; p.bk = 128; break;
   }
-  if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0) {  // same tile family, k step 64
-    p.kind = p.kind == K_DMA_128x128 ? K_DMA_256x128 : K_TILE_128x256;
-    p.bm = p.kind == K_DMA_256x128 ? 256 : 128;
-    p.bn = p.kind == K_DMA_256x128 ? 128 : 256;
-    p.bk = 64;
+  if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0 && p.kind != K_TILE_128x128) {
+    p.kind = K_DMA_256x128;  // same family, k step 64
+    p.bm = 256; p.bn = 128; p.bk = 64;
   }
   if (K % p.bk != 0) {  // fall back to a k step that divides K
     p.kind = K_TILE_128x128;
-    p.bm = 128; p.bn = 128; p.bk = 32;
+    p.bm = 128; p.bn = 128; p.bk = K % 128 == 0 ? 128 : 32;
     if (K % 32 != 0) { p.kind = K_SCALAR; return p; }
   }
   p.splits = 1;
@@ -637,26 +756,33 @@ template <int EPI>
 void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
                  const EpiArgs& ep, hipStream_t st) {
   const dim3 block(256);
-  const dim3 grid((unsigned)ceil_div(N, p.bn), (unsigned)ceil_div(M, p.bm), (unsigned)p.splits);
-  if (p.kind == K_DMA_256x256) {
-    gemm_dma<256, 256, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_DMA_128x256) {
-    gemm_dma<128, 256, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_DMA_256x128) {
-    gemm_dma<256, 128, 64, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_DMA_128x128) {
-    gemm_dma<128, 128, 128, 2, 2, 4, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_TILE_256x256) {
-    gemm_tile<256, 256, 64, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_TILE_128x256) {
-    gemm_tile<128, 256, 64, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.kind == K_TILE_64x128) {
-    gemm_tile<64, 128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else if (p.bk == 32) {
-    gemm_tile<128, 128, 32, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
-  } else {
-    gemm_tile<128, 128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+  if (p.kind == K_TILE_128x128) {
+    const dim3 grid((unsigned)ceil_div(N, p.bn), (unsigned)ceil_div(M, p.bm), (unsigned)p.splits);
+    if (p.bk == 32) gemm_tile<128, 128, 32, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+    else gemm_tile<128, 128, 128, 2, 2, EPI><<<grid, block, 0, st>>>(a, b, M, N, K, p.k_split, c, ep);
+    return;
   }
+  // DMA kernels: one linear grid dimension over the tiles (renumbered per XCD
+  // inside the kernel), splits in z.
+  const dim3 grid((unsigned)(ceil_div(M, p.bm) * ceil_div(N, p.bn)), 1, (unsigned)p.splits);
+#define SI_DMA(BM_, BN_, BK_, WM_, WN_, S_)                                                    \
+  gemm_dma<BM_, BN_, BK_, WM_, WN_, S_, EPI><<<grid, dim3(64 * WM_ * WN_), 0, st>>>( \
+      a, b, M, N, K, p.k_split, c, ep)
+  switch (p.kind) {
+    case K_DMA_256x256: SI_DMA(256, 256, 64, 2, 2, 4); break;
+    case K_DMA_128x256: SI_DMA(128, 256, 64, 2, 2, 4); break;
+    case K_DMA_256x128: SI_DMA(256, 128, 64, 2, 2, 4); break;
+    case K_DMA_128x128: SI_DMA(128, 128, 128, 2, 2, 4); break;
+    case K_DMA_256x192: SI_DMA(256, 192, 64, 2, 2, 4); break;
+    case K_DMA_256x64: SI_DMA(256, 64, 128, 4, 1, 3); break;
+    case K_DMA_256x128_K128: SI_DMA(256, 128, 128, 2, 2, 3); break;
+    case K_DMA8_256x256: SI_DMA(256, 256, 64, 4, 2, 4); break;
+    case K_DMA8_256x256_K128: SI_DMA(256, 256, 128, 4, 2, 2); break;
+    case K_DMA8_256x192_K128: SI_DMA(256, 192, 128, 4, 2, 2); break;
+    case K_DMA8_256x128: SI_DMA(256, 128, 64, 4, 2, 4); break;
+    default: SI_DMA(128, 256, 64, 2, 4, 4); break;
+  }
+#undef SI_DMA
 }
 
 template <int EPI>
@@ -688,6 +814,12 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
              EpiArgs ep, bool dequant, void* ws, size_t ws_bytes, hipStream_t st, const char* who) {
   if (M == 0 || N == 0) return SI_OK;
   const Plan p = choose(M, N, K);
+  {
+    uintptr_t bits = reinterpret_cast<uintptr_t>(c) | reinterpret_cast<uintptr_t>(ep.out) |
+                     reinterpret_cast<uintptr_t>(ep.sw) | reinterpret_cast<uintptr_t>(ep.bias) |
+                     reinterpret_cast<uintptr_t>(ws);
+    ep.vec = (N % 8 == 0 && (bits & 15) == 0) ? 1 : 0;
+  }
   if (p.kind == K_SCALAR) {
     const int64_t blocks = std::min<int64_t>(ceil_div(M * N, 256), 65536);
     gemm_i8_scalar<<<(unsigned)blocks, 256, 0, st>>>(a, b, M, N, K, c, ep, dequant ? 1 : 0);

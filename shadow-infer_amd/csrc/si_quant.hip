@@ -245,6 +245,79 @@ extern "C" int si_dequant_rows(const int8_t* q, const void* scale, int scale_dty
   return check_launch("si_dequant_rows");
 }
 
+// Vector form of act_quant_kernel for rows of K % 8 == 0 elements (16-byte
+// aligned rows, K <= 2048 * R): one block per row, the row held in registers
+// (R chunks of 8 values per thread), 16-byte loads and 8-byte int8 stores.
+// Same arithmetic: amax, s = max(amax / 127, 1e-8), q = clamp(rint(x / s), +-127)
+// with the IEEE division.
+template <int DT, int R>
+__global__ __launch_bounds__(256) void act_quant_vec(const void* __restrict__ x, int64_t M, int K,
+                                                      int8_t* __restrict__ q,
+                                                      float* __restrict__ scale) {
+  __shared__ float lds[4];
+  const float eps = 1e-8f;
+  const int nch = K / 8;
+  for (int64_t m = blockIdx.x; m < M; m += gridDim.x) {
+    float v[R][8];
+    float a = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = (int)threadIdx.x + r * 256;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[r][e] = 0.0f;
+      if (c < nch) {
+        const int64_t base = m * K + (int64_t)c * 8;
+        if constexpr (DT == SI_DT_F32) {
+          const float4 lo = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + base)[0];
+          const float4 hi = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + base)[1];
+          v[r][0] = lo.x; v[r][1] = lo.y; v[r][2] = lo.z; v[r][3] = lo.w;
+          v[r][4] = hi.x; v[r][5] = hi.y; v[r][6] = hi.z; v[r][7] = hi.w;
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + base);
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (DT == SI_DT_BF16) {
+              v[r][2 * e] = bf16_bits_to_f32(ws[e] & 0xffffu);
+              v[r][2 * e + 1] = bf16_bits_to_f32(ws[e] >> 16);
+            } else {
+              v[r][2 * e] = f16_bits_to_f32(ws[e] & 0xffffu);
+              v[r][2 * e + 1] = f16_bits_to_f32(ws[e] >> 16);
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a = amax_fold(a, v[r][e]);
+      }
+    }
+    a = block_amax(a, lds);
+    float s = a / 127.0f;
+    s = s < eps ? eps : s;  // clamp_min(1e-8); NaN passes through like torch
+    if (threadIdx.x == 0) scale[m] = s;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = (int)threadIdx.x + r * 256;
+      if (c >= nch) continue;
+      uint32_t b[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float t = rintf(v[r][e] / s);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        b[e >> 2] |= ((uint32_t)(int)t & 0xffu) << (8 * (e & 3));
+      }
+      *reinterpret_cast<uint2*>(q + m * K + (int64_t)c * 8) = make_uint2(b[0], b[1]);
+    }
+  }
+}
+
+template <int DT>
+void launch_act_quant_vec(const void* x, int64_t M, int K, int8_t* q, float* scale, unsigned grid,
+                          hipStream_t st) {
+  if (K <= 2048) act_quant_vec<DT, 1><<<grid, 256, 0, st>>>(x, M, K, q, scale);
+  else if (K <= 4096) act_quant_vec<DT, 2><<<grid, 256, 0, st>>>(x, M, K, q, scale);
+  else act_quant_vec<DT, 4><<<grid, 256, 0, st>>>(x, M, K, q, scale);
+}
+
 extern "C" int si_act_quant_i8(const void* x, int dtype, int64_t M, int64_t K, int8_t* q,
                                float* scale, si_stream_t stream) {
   clear_error();
@@ -253,7 +326,19 @@ extern "C" int si_act_quant_i8(const void* x, int dtype, int64_t M, int64_t K, i
   if (M == 0) return SI_OK;
   SI_CHECK_ARG(x && q && scale, "si_act_quant_i8: NULL argument");
   const unsigned grid = (unsigned)(M < 65536 ? M : 65536);
-  act_quant_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, dtype, M, K, q, scale);
+  const size_t esz = dtype == SI_DT_F32 ? 4 : 2;
+  const bool vec = K % 8 == 0 && K <= 8192 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(q) & 7) == 0 && ((size_t)K * esz) % 16 == 0;
+  hipStream_t st = as_stream(stream);
+  if (!vec) {
+    act_quant_kernel<<<grid, 256, 0, st>>>(x, dtype, M, K, q, scale);
+  } else if (dtype == SI_DT_BF16) {
+    launch_act_quant_vec<SI_DT_BF16>(x, M, (int)K, q, scale, grid, st);
+  } else if (dtype == SI_DT_F16) {
+    launch_act_quant_vec<SI_DT_F16>(x, M, (int)K, q, scale, grid, st);
+  } else {
+    launch_act_quant_vec<SI_DT_F32>(x, M, (int)K, q, scale, grid, st);
+  }
   return check_launch("si_act_quant_i8");
 }
 

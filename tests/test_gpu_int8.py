@@ -79,7 +79,8 @@ def test_gemm_extreme_values_no_overflow(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
-@pytest.mark.parametrize("M,K", [(16, 4096), (7, 128), (1024, 4096)])
+@pytest.mark.parametrize("M,K", [(16, 4096), (7, 128), (1024, 4096), (5, 2048), (2, 8192),
+                                 (3, 11008), (4, 100), (9, 3000)])
 def test_act_quant_bit_exact(dev, dtype, M, K):
     g = torch.Generator().manual_seed(M + K)
     x = torch.randn(M, K, generator=g).to(dtype)
