@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SI_ABI_VERSION 1
+#define SI_ABI_VERSION 2
 
 #define SI_OK 0
 #define SI_ERR_INVALID 1
@@ -133,17 +133,22 @@ int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
                   const int32_t* new_slot, void* const* new_buckets, int64_t n_entries,
                   int64_t B, int64_t D, int64_t group, int scale_dtype, si_stream_t stream);
 
+/* Bytes of device workspace si_attn_packed_fwd needs (per-head slot lists). */
+size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv);
+
 /* Replaces unpack() -> softmax(q k^T * sm_scale) v with no mask
  * (shadowinfer/models/simple_diffusion_llm.py:165-169) as one fused kernel
  * that dequantizes packed K/V tiles into LDS; the dense K/V never exist.
  * Semantic neighbour of shadowinfer/kernels/__init__.py:473-537.
- * q: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16; D = 64 or 128.
- * out: [B, H, S_q, D] in out_dtype (SI_DT_F32 matches unpack()'s fp32 K/V). */
+ * q: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16, 16-byte aligned; D = 64
+ * or 128; group: int4 group size (a multiple of D/16 dividing D).
+ * out: [B, H, S_q, D] in out_dtype (SI_DT_F32 matches unpack()'s fp32 K/V).
+ * workspace: si_attn_workspace_bytes(H, S_kv) bytes, 16-byte aligned. */
 int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
                        int64_t D, const int8_t* code, const int32_t* slot,
                        const void* const* buckets, int scale_dtype, int64_t S_kv,
                        int64_t group, float sm_scale, void* out, int out_dtype,
-                       si_stream_t stream);
+                       void* workspace, size_t workspace_bytes, si_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Quantizer                                                               */

@@ -28,29 +28,193 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128;  // queries per block
 constexpr int BN = 64;   // keys per tile
-constexpr int KPAD = 8;  // fp16 padding per LDS row
+constexpr int KPAD = 8;  // fp16 padding per K row in LDS
 
-template <int QDT>
-__device__ __forceinline__ _Float16 q_to_h(uint32_t bits) {
-  const float f = QDT == SI_DT_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
-  return (_Float16)f;
+// Capacity of one head's slot list: every precision region starts at a multiple of BN.
+inline int64_t list_cap(int64_t Skv) { return (Skv + BN - 1) / BN * BN + 4 * BN; }
+
+// ---------------------------------------------------------------------------
+// Per-head slot lists. Softmax attention without a mask does not depend on the
+// order of the keys, so the attention kernel visits each head's keys bucket
+// by bucket: tiles then hold one precision (branch-free decode, contiguous
+// rows). For head h: lists[h * cap + off_p + i] = slot of the i-th entry of
+// precision p (token order), off_p = sum over q < p of n_q rounded up to BN;
+// counts[h * 8 + p] = n_p, counts[h * 8 + 4] = keys that are evicted or absent
+// (they attend as zero vectors: score 0, value 0).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_lists(const int8_t* __restrict__ code,
+                                                  const int32_t* __restrict__ slot, int64_t H,
+                                                  int64_t Skv, int64_t cap,
+                                                  int32_t* __restrict__ counts,
+                                                  int32_t* __restrict__ lists) {
+  __shared__ int wtot[5][4];
+  const int64_t h = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t per = (Skv + 255) / 256;
+  const int64_t t0 = min<int64_t>(Skv, tid * per), t1 = min<int64_t>(Skv, t0 + per);
+  int n[5] = {0, 0, 0, 0, 0};
+  for (int64_t t = t0; t < t1; ++t) {
+    const int c = code[t * H + h];
+    ++n[(c >= 0 && c <= 3) ? c : 4];
+  }
+  // Exclusive prefix of each counter over the threads (token order).
+  int pre[5];
+#pragma unroll
+  for (int p = 0; p < 5; ++p) {
+    int v = n[p];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(v, o, 64);
+      if (lane >= o) v += u;
+    }
+    pre[p] = v - n[p];
+    if (lane == 63) wtot[p][wave] = v;
+  }
+  __syncthreads();
+  int tot[5];
+#pragma unroll
+  for (int p = 0; p < 5; ++p) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      before += w < wave ? wtot[p][w] : 0;
+      all += wtot[p][w];
+    }
+    pre[p] += before;
+    tot[p] = all;
+  }
+  int off[4];
+  off[0] = 0;
+#pragma unroll
+  for (int p = 1; p < 4; ++p) off[p] = off[p - 1] + (tot[p - 1] + BN - 1) / BN * BN;
+  int32_t* lh = lists + h * cap;
+  for (int64_t t = t0; t < t1; ++t) {
+    const int64_t e = t * H + h;
+    const int c = code[e];
+    if (c >= 0 && c <= 3) lh[off[c] + pre[c]++] = slot[e];
+  }
+  if (tid == 0) {
+#pragma unroll
+    for (int p = 0; p < 5; ++p) counts[h * 8 + p] = tot[p];
+  }
 }
 
+template <int QDT>
+__device__ __forceinline__ float q_to_f(uint32_t bits) {
+  return QDT == SI_DT_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
 
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+// NB bytes at p (aligned to NB) into 32-bit words.
+template <int NB>
+__device__ __forceinline__ void load_raw(const void* p, uint32_t* r) {
+  if constexpr (NB == 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+  } else if constexpr (NB == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    r[0] = v.x; r[1] = v.y;
+  } else if constexpr (NB == 4) {
+    r[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (NB == 2) {
+    r[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else {
+    r[0] = *reinterpret_cast<const uint8_t*>(p);
+  }
+}
+
+template <int D>
+struct AttnCfg {
+  static constexpr int NW = 8;              // waves per block (two per SIMD)
+  static constexpr int BMQ = 32 * NW;       // queries per block
+  static constexpr int DPT = D / (4 * NW);  // head-dim values per thread in the decode stage
+  static constexpr int DGN = 4 * NW;        // dim groups (threads per key group)
+  static constexpr int RW = DPT / 2;        // 32-bit words of one key's fp16 values
+  // V^T pitch (fp16) and store rotation that keep the transposed 8-byte stores
+  // at two LDS passes per 32 lanes.
+  static constexpr int VPITCH = 76;
+};
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2 as_h2(uint32_t w) { return __builtin_bit_cast(h2, w); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Bytes b0..b3 of w (two's-complement int8) as fp16 integer pairs
+// {b0, b1}, {b2, b3}: 0x64xx is the fp16 1024 + xx, so (w ^ 0x80) bytes give
+// 1024 + q + 128 exactly, minus 1152.
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+  hi = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+
+// The low two bytes of w (int4 pairs, high nibble first, offset-binary q + 8)
+// as fp16 integer pairs {e0, e1}, {e2, e3}.
+__device__ __forceinline__ void i4x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t hn = (w >> 4) & 0x0f0fu;  // bytes: e0, e2
+  const uint32_t ln = w & 0x0f0fu;         // bytes: e1, e3
+  const uint32_t n = __builtin_amdgcn_perm(hn, ln, 0x01050004u);  // e0, e1, e2, e3
+  const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+  lo = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, n, 0x04010400u)) - bias);
+  hi = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, n, 0x04030402u)) - bias);
+}
+
+// fp16 copy of a scale when fp16(q) * fp16(s) rounds exactly like
+// fp16(float(q) * float(s)): s exact in fp16, normal, and |q * s| <= 65504
+// for |q| <= qmax. Otherwise 0 (callers take the fp32 route).
+__device__ __forceinline__ _Float16 exact_h(float s, float qmax) {
+  const _Float16 hs = (_Float16)s;
+  const bool ok = (float)hs == s && s >= 6.103515625e-05f && s * qmax <= 65504.0f;
+  return ok ? hs : (_Float16)0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Fused dequantize + bidirectional attention over a packed KV cache.
+//
+// out = softmax(q k^T * sm_scale) v with no mask, k/v being the values
+// PackedKVCache.unpack() produces (packed_kv_cache.py:535-577); evicted or
+// absent token-heads are zero vectors that still take part in the softmax,
+// as in unpack() -> dense attention (models/simple_diffusion_llm.py:165-169).
+// The dense K/V never exist: each 64-key tile is decoded into LDS as fp16.
+//
+// One block of 8 waves (two per SIMD) owns 256 queries of one (b, h); each
+// wave owns 32. Tiles follow the head's slot list (one precision per tile).
+// Per tile:
+//  * decode (512 threads, 4 keys x D/32 dims each) from registers loaded one
+//    tile ahead (slot lists two tiles ahead), K row-major and V transposed;
+//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: lane l holds scores of query
+//    l % 32 for 16 keys (lane l ^ 32 the other 16);
+//  * int8 K tiles keep the raw integers in LDS (exact in fp16) and apply the
+//    per-key scale to the score in fp32: exact arithmetic on the reference's
+//    float(q) * float(s) dequantization;
+//  * online softmax in the log2 domain; the running max is only raised when a
+//    score exceeds it by more than 2^8 (probabilities stay <= 256), so the
+//    output rescale is rare;
+//  * O^T += V^T P^T reuses the score registers as the B operand (the k order
+//    of an MFMA only has to agree between A and B: V^T is read in the score
+//    accumulator's key order 8*(i/4) + 4*(l/32) + i%4).
+// Evicted/absent keys have score 0; they are added to the softmax
+// denominator at the end (n_ev * 2^(0 - m)).
+// ---------------------------------------------------------------------------
 template <int D, int SDT, int QDT>
-__global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restrict__ Q,
-                                                       int64_t B, int64_t H, int64_t Sq,
-                                                       int64_t Skv, const int8_t* __restrict__ code,
-                                                       const int32_t* __restrict__ slot,
-                                                       Buckets bk, int64_t g, float scale_log2,
-                                                       void* __restrict__ O, int odt) {
-  constexpr int KS = D / 16;   // MFMA k-steps over the head dim
-  constexpr int DB = D / 32;   // 32-row blocks of O^T
-  constexpr int DPT = D / 4;   // head-dim values per thread in the dequant stage
+__global__ __launch_bounds__(512) void attn_packed_fwd(
+    const uint16_t* __restrict__ Q, int64_t B, int64_t H, int64_t Sq, int64_t cap,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ lists, Buckets bk, int64_t g,
+    float scale_log2, void* __restrict__ O, int odt) {
+  using C = AttnCfg<D>;
+  constexpr int KS = D / 16;  // MFMA k-steps over the head dim
+  constexpr int DB = D / 32;  // 32-row blocks of O^T
+  constexpr int DPT = C::DPT, RW = C::RW > 0 ? C::RW : 1;
+  constexpr int VP = C::VPITCH;
   __shared__ __attribute__((aligned(16))) _Float16 Ks[BN][D + KPAD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[D][BN + KPAD];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[D][VP];
+  __shared__ __attribute__((aligned(16))) float ksc[BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -59,7 +223,7 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
   const int grp = lane >> 5;  // 0/1: k-half of MFMA operands, row quad of results
   const int64_t h = blockIdx.y;
   const int64_t b = blockIdx.z;
-  const int64_t m = (int64_t)blockIdx.x * BM + wave * 32 + col;
+  const int64_t m = (int64_t)blockIdx.x * C::BMQ + wave * 32 + col;
   const bool m_ok = m < Sq;
 
   // Q^T fragments (B operand of S^T = K Q^T): query m, dims ks*16 + 8*grp + 0..7.
@@ -73,11 +237,74 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
       const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        qf[ks][2 * i] = q_to_h<QDT>(w[i] & 0xffffu);
-        qf[ks][2 * i + 1] = q_to_h<QDT>(w[i] >> 16);
+        qf[ks][2 * i] = (_Float16)(q_to_f<QDT>(w[i] & 0xffffu) * scale_log2);
+        qf[ks][2 * i + 1] = (_Float16)(q_to_f<QDT>(w[i] >> 16) * scale_log2);
       }
     }
   }
+
+  // Tile schedule: the head's list regions in order fp32, fp16, int8, int4.
+  const int32_t* cnt = counts + h * 8;
+  int np[4], tstart[5];
+  tstart[0] = 0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    np[p] = cnt[p];
+    tstart[p + 1] = tstart[p] + (np[p] + BN - 1) / BN;
+  }
+  const int n_ev = cnt[4];
+  const int T = tstart[4];
+  const int32_t* lh = lists + h * cap;
+  auto tile_prec = [&](int tt) {
+    return tt < tstart[1] ? 0 : tt < tstart[2] ? 1 : tt < tstart[3] ? 2 : 3;
+  };
+  auto tile_valid = [&](int tt, int p) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
+
+  // Decode-stage coordinates: keys 4*kg .. 4*kg+3 of the tile, dims d0 .. d0+DPT-1.
+  const int kg = tid / C::DGN;
+  const int dg = tid % C::DGN;
+  const int d0 = dg * DPT;
+
+  int4 sl = make_int4(0, 0, 0, 0);  // slots of the next tile to fetch
+  int4 sl_data = sl;                 // slots of the tile held in rk / rv
+  uint32_t rk[4][RW], rv[4][RW];
+  float sk[4], sv[4];
+
+  auto fetch_slots = [&](int tt) {
+    sl = *reinterpret_cast<const int4*>(lh + (int64_t)tt * BN + 4 * kg);
+  };
+  // Raw loads of the tile's rows into registers (fp32 tiles are read at decode time).
+  auto fetch_data = [&](int tt) {
+    const int p = __builtin_amdgcn_readfirstlane(tile_prec(tt));
+    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, p));
+    sl_data = sl;
+    const int sl4[4] = {sl.x, sl.y, sl.z, sl.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int w = 0; w < RW; ++w) rk[i][w] = rv[i][w] = 0u;
+      sk[i] = sv[i] = 0.0f;
+      if (4 * kg + i >= nv || p == SI_PREC_FP32) continue;
+      const int64_t row = (int64_t)sl4[i] * B + b;
+      if (p == SI_PREC_FP16) {
+        load_raw<2 * DPT>(reinterpret_cast<const uint16_t*>(bk.p[4]) + row * D + d0, rk[i]);
+        load_raw<2 * DPT>(reinterpret_cast<const uint16_t*>(bk.p[5]) + row * D + d0, rv[i]);
+      } else if (p == SI_PREC_INT8) {
+        load_raw<DPT>(reinterpret_cast<const int8_t*>(bk.p[8]) + row * D + d0, rk[i]);
+        load_raw<DPT>(reinterpret_cast<const int8_t*>(bk.p[9]) + row * D + d0, rv[i]);
+        sk[i] = load_scale<SDT>(bk.p[10], row);
+        sv[i] = load_scale<SDT>(bk.p[11], row);
+      } else {
+        const int64_t rb = B * D / 2;  // bytes of one int4 entry row
+        const int64_t off = sl4[i] * rb + (b * D + d0) / 2;
+        load_raw<DPT / 2>(reinterpret_cast<const uint8_t*>(bk.p[12]) + off, rk[i]);
+        load_raw<DPT / 2>(reinterpret_cast<const uint8_t*>(bk.p[13]) + off, rv[i]);
+        const int64_t si = row * (D / g) + d0 / g;
+        sk[i] = load_scale<SDT>(bk.p[14], si);
+        sv[i] = load_scale<SDT>(bk.p[15], si);
+      }
+    }
+  };
 
   v16f o[DB];
 #pragma unroll
@@ -87,44 +314,166 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
-  const int dj = tid >> 2;          // key of this thread in the dequant stage
-  const int dd = (tid & 3) * DPT;   // first head-dim value of this thread
-
-  for (int64_t kv0 = 0; kv0 < Skv; kv0 += BN) {
-    // ---- dequantize the K/V tile into LDS ----
-    __syncthreads();
+  if (T > 0) {
+    fetch_slots(0);
+    fetch_data(0);
+    if (T > 1) fetch_slots(1);
+  }
+  for (int tt = 0; tt < T; ++tt) {
+    const int p = __builtin_amdgcn_readfirstlane(tile_prec(tt));  // block-uniform
+    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, p));
+    // ---- decode the tile into LDS ----
+    __syncthreads();  // the previous tile's MFMAs are done with Ks / Vt / ksc
     {
-      const int64_t t = kv0 + dj;
-      int c = SI_PREC_EVICTED;
-      int64_t s = 0;
-      if (t < Skv) {
-        const int64_t e = t * H + h;
-        c = code[e];
-        if (c >= 0 && c <= 3) s = slot[e];
-      }
-      const bool present = c >= 0 && c <= 3;
-#pragma unroll
-      for (int d4 = 0; d4 < DPT; d4 += 4) {
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-        if (present) {
-          kv = dequant4<SDT>(bk, 0, c, s, b, dd + d4, B, D, g);
-          vv = dequant4<SDT>(bk, 1, c, s, b, dd + d4, B, D, g);
+      uint32_t vt[DPT][2];  // V^T words: [e][0] = keys 0,1, [e][1] = keys 2,3 of dim d0 + e
+      auto put_k = [&](int i, const uint32_t* w) {
+        if constexpr (DPT == 8) {
+          *reinterpret_cast<uint4*>(&Ks[4 * kg + i][d0]) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else if constexpr (DPT == 4) {
+          *reinterpret_cast<uint2*>(&Ks[4 * kg + i][d0]) = make_uint2(w[0], w[1]);
+        } else {
+          *reinterpret_cast<uint32_t*>(&Ks[4 * kg + i][d0]) = w[0];
         }
-        v4h kh;
-        kh[0] = (_Float16)kv.x;
-        kh[1] = (_Float16)kv.y;
-        kh[2] = (_Float16)kv.z;
-        kh[3] = (_Float16)kv.w;
-        *reinterpret_cast<v4h*>(&Ks[dj][dd + d4]) = kh;
-        Vt[dd + d4 + 0][dj] = (_Float16)vv.x;
-        Vt[dd + d4 + 1][dj] = (_Float16)vv.y;
-        Vt[dd + d4 + 2][dj] = (_Float16)vv.z;
-        Vt[dd + d4 + 3][dj] = (_Float16)vv.w;
+      };
+      auto put_v = [&](int i, int e, _Float16 x) {
+        const uint32_t hx = __builtin_bit_cast(uint16_t, x);
+        uint32_t& w = vt[e][i >> 1];
+        w = (i & 1) ? ((w & 0xffffu) | (hx << 16)) : ((w & 0xffff0000u) | hx);
+      };
+      if (p == SI_PREC_FP16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) put_k(i, rk[i]);
+#pragma unroll
+        for (int w = 0; w < RW; ++w) {
+          vt[2 * w][0] = __builtin_amdgcn_perm(rv[1][w], rv[0][w], 0x05040100u);
+          vt[2 * w][1] = __builtin_amdgcn_perm(rv[3][w], rv[2][w], 0x05040100u);
+          vt[2 * w + 1][0] = __builtin_amdgcn_perm(rv[1][w], rv[0][w], 0x07060302u);
+          vt[2 * w + 1][1] = __builtin_amdgcn_perm(rv[3][w], rv[2][w], 0x07060302u);
+        }
+      } else if (p == SI_PREC_INT8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // K keeps the integer values (exact in fp16); the scale multiplies the score.
+          uint32_t w[RW];
+#pragma unroll
+          for (int x = 0; x < DPT / 4; ++x) i8x4_to_h(rk[i][x], w[2 * x], w[2 * x + 1]);
+          if constexpr (DPT == 2) {
+            uint32_t unused;
+            i8x4_to_h(rk[i][0], w[0], unused);
+          }
+          put_k(i, w);
+          // V: float(q) * float(s) rounded to fp16
+          const _Float16 hs = exact_h(sv[i], 128.0f);
+          if (hs != (_Float16)0.0f) {
+            const h2 s2 = {hs, hs};
+            uint32_t q[RW];
+#pragma unroll
+            for (int x = 0; x < DPT / 4; ++x) i8x4_to_h(rv[i][x], q[2 * x], q[2 * x + 1]);
+            if constexpr (DPT == 2) {
+              uint32_t unused;
+              i8x4_to_h(rv[i][0], q[0], unused);
+            }
+#pragma unroll
+            for (int x = 0; x < RW; ++x) {
+              const h2 v = as_h2(q[x]) * s2;
+              put_v(i, 2 * x, v[0]);
+              put_v(i, 2 * x + 1, v[1]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) {
+              const float qv = (float)(int8_t)((rv[i][e >> 2] >> (8 * (e & 3))) & 0xffu);
+              put_v(i, e, (_Float16)(qv * sv[i]));
+            }
+          }
+        }
+      } else if (p == SI_PREC_INT4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // float(q) * float(s) rounded to fp16, for K and V
+          const _Float16 hk = exact_h(sk[i], 8.0f), hv = exact_h(sv[i], 8.0f);
+          uint32_t w[RW];
+          if constexpr (DPT >= 4) {
+#pragma unroll
+            for (int x = 0; x < DPT / 4; ++x) {
+              uint32_t qlo, qhi;
+              i4x4_to_h(rk[i][0] >> (16 * x), qlo, qhi);
+              if (hk != (_Float16)0.0f) {
+                const h2 s2 = {hk, hk};
+                w[2 * x] = as_u32(as_h2(qlo) * s2);
+                w[2 * x + 1] = as_u32(as_h2(qhi) * s2);
+              } else {
+                const h2 a = as_h2(qlo), c = as_h2(qhi);
+                w[2 * x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
+                w[2 * x + 1] = pack_h2((_Float16)((float)c[0] * sk[i]), (_Float16)((float)c[1] * sk[i]));
+              }
+              i4x4_to_h(rv[i][0] >> (16 * x), qlo, qhi);
+              const h2 a = as_h2(qlo), c = as_h2(qhi);
+              if (hv != (_Float16)0.0f) {
+                const h2 s2 = {hv, hv};
+                const h2 va = a * s2, vc = c * s2;
+                put_v(i, 4 * x + 0, va[0]);
+                put_v(i, 4 * x + 1, va[1]);
+                put_v(i, 4 * x + 2, vc[0]);
+                put_v(i, 4 * x + 3, vc[1]);
+              } else {
+                put_v(i, 4 * x + 0, (_Float16)((float)a[0] * sv[i]));
+                put_v(i, 4 * x + 1, (_Float16)((float)a[1] * sv[i]));
+                put_v(i, 4 * x + 2, (_Float16)((float)c[0] * sv[i]));
+                put_v(i, 4 * x + 3, (_Float16)((float)c[1] * sv[i]));
+              }
+            }
+          } else {
+            const uint32_t kb = rk[i][0] & 0xffu, vb = rv[i][0] & 0xffu;
+            w[0] = pack_h2((_Float16)((float)((int)(kb >> 4) - 8) * sk[i]),
+                           (_Float16)((float)((int)(kb & 0xfu) - 8) * sk[i]));
+            put_v(i, 0, (_Float16)((float)((int)(vb >> 4) - 8) * sv[i]));
+            put_v(i, 1, (_Float16)((float)((int)(vb & 0xfu) - 8) * sv[i]));
+          }
+          put_k(i, w);
+        }
+      } else {  // fp32 bucket rows, read here
+        const int sl4[4] = {sl_data.x, sl_data.y, sl_data.z, sl_data.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float kx[DPT], vx[DPT];
+#pragma unroll
+          for (int e = 0; e < DPT; ++e) kx[e] = vx[e] = 0.0f;
+          if (4 * kg + i < nv) {
+            const int64_t row = (int64_t)sl4[i] * B + b;
+            const float* kp = reinterpret_cast<const float*>(bk.p[0]) + row * D + d0;
+            const float* vp = reinterpret_cast<const float*>(bk.p[1]) + row * D + d0;
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) {
+              kx[e] = kp[e];
+              vx[e] = vp[e];
+            }
+          }
+          uint32_t w[RW];
+#pragma unroll
+          for (int e = 0; e < DPT; e += 2) w[e >> 1] = pack_h2((_Float16)kx[e], (_Float16)kx[e + 1]);
+          put_k(i, w);
+#pragma unroll
+          for (int e = 0; e < DPT; ++e) put_v(i, e, (_Float16)vx[e]);
+        }
       }
+      if (dg == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ksc[4 * kg + i] = p == SI_PREC_INT8 ? sk[i] : 1.0f;
+      }
+      // V^T rows d0 + e hold keys 4*kg .. 4*kg+3 (8 bytes).
+#pragma unroll
+      for (int e = 0; e < DPT; ++e)
+        *reinterpret_cast<uint2*>(&Vt[d0 + e][4 * kg]) = make_uint2(vt[e][0], vt[e][1]);
     }
     __syncthreads();
+    // ---- prefetch: rows of the next tile, slots of the one after ----
+    if (tt + 1 < T) {
+      fetch_data(tt + 1);
+      if (tt + 2 < T) fetch_slots(tt + 2);
+    }
 
-    // ---- S^T = K Q^T for keys kv0 + [0, 64) ----
+    // ---- S^T = K Q^T for the tile's 64 keys ----
     v16f sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -137,39 +486,56 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
       }
     }
 
-    // ---- online softmax (log2 domain) ----
-    float tmax = -INFINITY;
+    // ---- online softmax (log2 domain; Q carries sm_scale * log2(e)) ----
+    if (p == SI_PREC_INT8) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb * 32 + 8 * (r >> 2) + 4 * grp + (r & 3);
-        float v = sacc[kb][r] * scale_log2;
-        if (kv0 + key >= Skv) v = -INFINITY;
-        sacc[kb][r] = v;
-        tmax = fmaxf(tmax, v);
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 f = *reinterpret_cast<const float4*>(&ksc[kb * 32 + 8 * q4 + 4 * grp]);
+          sacc[kb][4 * q4 + 0] *= f.x;
+          sacc[kb][4 * q4 + 1] *= f.y;
+          sacc[kb][4 * q4 + 2] *= f.z;
+          sacc[kb][4 * q4 + 3] *= f.w;
+        }
       }
     }
+    if (nv < BN) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb * 32 + 8 * (r >> 2) + 4 * grp + (r & 3) >= nv) sacc[kb][r] = -INFINITY;
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[kb][r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
+    const bool raise = tmax > m_run + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float m_new = raise ? tmax : m_run;
+      const float alpha = exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      m_run = m_new;
+    }
     float psum = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(sacc[kb][r] - m_new);
-        sacc[kb][r] = p;
-        psum += p;
+        // v_exp_f32: arguments are <= 8 here; results below 2^-126 flush to 0
+        const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_run);
+        sacc[kb][r] = pr;
+        psum += pr;
       }
     }
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < DB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    l_run += psum + __shfl_xor(psum, 32, 64);
 
     // ---- O^T += V^T P^T over four 16-key chunks ----
 #pragma unroll
@@ -188,6 +554,17 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[db], 0, 0, 0);
       }
     }
+  }
+
+  // Evicted / absent keys: score 0, value 0.
+  if (n_ev > 0) {
+    const float m_fin = fmaxf(m_run, 0.0f);
+    const float alpha = exp2f(m_run - m_fin);
+    l_run = l_run * alpha + (float)n_ev * exp2f(-m_fin);
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
   }
 
   if (!m_ok) return;
@@ -217,20 +594,21 @@ __global__ __launch_bounds__(256) void attn_packed_fwd(const uint16_t* __restric
 
 template <int D, int QDT>
 void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t B, int64_t H,
-                 int64_t Sq, int64_t Skv, const int8_t* code, const int32_t* slot,
+                 int64_t Sq, int64_t cap, const int32_t* counts, const int32_t* lists,
                  const Buckets& bk, int64_t g, float scale_log2, void* out, int odt) {
+  constexpr int NT = 64 * AttnCfg<D>::NW;
   switch (sdt) {
     case SI_DT_F32:
-      attn_packed_fwd<D, SI_DT_F32, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk, g,
-                                                               scale_log2, out, odt);
+      attn_packed_fwd<D, SI_DT_F32, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
+                                                              g, scale_log2, out, odt);
       break;
     case SI_DT_F16:
-      attn_packed_fwd<D, SI_DT_F16, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk, g,
-                                                               scale_log2, out, odt);
+      attn_packed_fwd<D, SI_DT_F16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
+                                                              g, scale_log2, out, odt);
       break;
     default:
-      attn_packed_fwd<D, SI_DT_BF16, QDT><<<grid, 256, 0, st>>>(q, B, H, Sq, Skv, code, slot, bk,
-                                                                g, scale_log2, out, odt);
+      attn_packed_fwd<D, SI_DT_BF16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
+                                                               bk, g, scale_log2, out, odt);
   }
 }
 
@@ -239,11 +617,16 @@ void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t 
 
 using namespace si;
 
+extern "C" size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv) {
+  if (H <= 0 || S_kv <= 0) return 0;
+  return (size_t)H * 8 * sizeof(int32_t) + (size_t)H * (size_t)list_cap(S_kv) * sizeof(int32_t);
+}
+
 extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
                                   int64_t D, const int8_t* code, const int32_t* slot,
                                   const void* const* buckets, int scale_dtype, int64_t S_kv,
                                   int64_t group, float sm_scale, void* out, int out_dtype,
-                                  si_stream_t stream) {
+                                  void* workspace, size_t workspace_bytes, si_stream_t stream) {
   clear_error();
   SI_CHECK_ARG(q_dtype == SI_DT_BF16 || q_dtype == SI_DT_F16,
                "si_attn_packed_fwd: q dtype must be bf16 or fp16 (got %d)", q_dtype);
@@ -253,29 +636,44 @@ extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t
   SI_CHECK_ARG(D == 64 || D == 128, "si_attn_packed_fwd: head_dim must be 64 or 128 (got %lld)",
                (long long)D);
   SI_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_kv > 0, "si_attn_packed_fwd: bad shape");
-  SI_CHECK_ARG(group > 0 && D % group == 0 && group % 4 == 0,
-               "si_attn_packed_fwd: int4 group must divide head_dim and be a multiple of 4");
-  SI_CHECK_ARG(H < 65536 && B < 65536, "si_attn_packed_fwd: H and B must be < 65536");
+  SI_CHECK_ARG(group > 0 && D % group == 0 && group % (D / 32) == 0,
+               "si_attn_packed_fwd: int4 group must divide head_dim and be a multiple of %lld",
+               (long long)(D / 32));
+  SI_CHECK_ARG(H < 65536 && B < 65536 && S_kv < ((int64_t)1 << 30),
+               "si_attn_packed_fwd: H and B must be < 65536, S_kv < 2^30");
   if (B * H * S_q == 0) return SI_OK;
   SI_CHECK_ARG(q && code && slot && buckets && out, "si_attn_packed_fwd: NULL argument");
+  const size_t need = si_attn_workspace_bytes(H, S_kv);
+  SI_CHECK_ARG(workspace != nullptr && workspace_bytes >= need &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+               "si_attn_packed_fwd: workspace too small or misaligned (%zu < %zu bytes)",
+               workspace_bytes, need);
+  SI_CHECK_ARG((reinterpret_cast<uintptr_t>(q) & 15) == 0,
+               "si_attn_packed_fwd: q must be 16-byte aligned");
   const Buckets bk = to_buckets(buckets);
-  const dim3 grid((unsigned)ceil_div(S_q, BM), (unsigned)H, (unsigned)B);
+  const int64_t cap = list_cap(S_kv);
+  int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+  int32_t* lists = counts + H * 8;
+  hipStream_t st = as_stream(stream);
+  attn_lists<<<(unsigned)H, 256, 0, st>>>(code, slot, H, S_kv, cap, counts, lists);
+  if (int rc = check_launch("si_attn_packed_fwd")) return rc;
+  const int64_t bmq = D == 128 ? AttnCfg<128>::BMQ : AttnCfg<64>::BMQ;
+  const dim3 grid((unsigned)ceil_div(S_q, bmq), (unsigned)H, (unsigned)B);
   const float scale_log2 = sm_scale * 1.4426950408889634f;
   const uint16_t* qp = reinterpret_cast<const uint16_t*>(q);
-  hipStream_t st = as_stream(stream);
   if (D == 128) {
     if (q_dtype == SI_DT_BF16)
-      launch_attn<128, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
+      launch_attn<128, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
                                    group, scale_log2, out, out_dtype);
     else
-      launch_attn<128, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
+      launch_attn<128, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
                                   group, scale_log2, out, out_dtype);
   } else {
     if (q_dtype == SI_DT_BF16)
-      launch_attn<64, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
+      launch_attn<64, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
                                   group, scale_log2, out, out_dtype);
     else
-      launch_attn<64, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, S_kv, code, slot, bk,
+      launch_attn<64, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
                                  group, scale_log2, out, out_dtype);
   }
   return check_launch("si_attn_packed_fwd");

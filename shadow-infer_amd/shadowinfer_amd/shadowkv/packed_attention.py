@@ -41,8 +41,10 @@ def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[f
         sm_scale = 1.0 / math.sqrt(D)
     qc = q.contiguous()
     out = torch.empty(qc.shape, dtype=out_dtype, device=qc.device)
+    ws_bytes = _native.size_query("si_attn_workspace_bytes", H, cache.seq_len)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=qc.device)
     _native.call("si_attn_packed_fwd", qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
                  code.data_ptr(), slot.data_ptr(), table, sdt, cache.seq_len, group,
-                 float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype),
-                 _native.stream(q.device))
+                 float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype), ws.data_ptr(),
+                 ws_bytes, _native.stream(q.device))
     return out

@@ -60,14 +60,20 @@ def test_argument_validation_needs_no_device():
     ws = _native.size_query("si_plan_workspace_bytes", 100)
     assert lib.si_plan_scan(1, null, 100, 1, 1, 1, 1, ws - 1, null) == 1
     assert b"workspace" in lib.si_last_error()
-    rc = lib.si_attn_packed_fwd(1, 2, 1, 1, 8, 96, 1, 1, table, 2, 8, 16, ctypes.c_float(0.1), 1, 0, null)
+    rc = lib.si_attn_packed_fwd(1, 2, 1, 1, 8, 96, 1, 1, table, 2, 8, 16, ctypes.c_float(0.1), 1, 0,
+                                1, 1 << 20, null)
     assert rc == 1 and b"head_dim" in lib.si_last_error()
+    ws = _native.size_query("si_attn_workspace_bytes", 2, 64)
+    rc = lib.si_attn_packed_fwd(16, 2, 1, 2, 8, 64, 1, 1, table, 2, 64, 16, ctypes.c_float(0.1), 16, 0,
+                                16, ws - 1, null)
+    assert rc == 1 and b"workspace" in lib.si_last_error()
     assert lib.si_int4_unpack_rows(1, 1, 2, 5, 1, null) == 1  # 2 bytes hold at most 4 codes
     with pytest.raises(ValueError, match="si_kv_unpack"):
         _native.call("si_kv_unpack", 1, 1, table, 2, 1, 1, 1, 64, 48, 1, 1, None)
 
 
 def test_workspace_queries():
+    assert _native.size_query("si_attn_workspace_bytes", 32, 8192) >= 32 * 8192 * 4
     assert _native.size_query("si_gemm_workspace_bytes", 16, 11008, 4096) > 0  # split-K
     assert _native.size_query("si_gemm_workspace_bytes", 2048, 11008, 4096) == 0
     assert _native.size_query("si_int8_linear_workspace_bytes", 16, 4096, 11008) >= 16 * 4096
