@@ -19,6 +19,8 @@
 // Precision: fp16 operands (10-bit mantissa) with fp32 accumulation and an
 // fp32 online softmax; fp16 entries of the cache are exact in fp16, int8/int4
 // values q*s are rounded once to fp16.
+#include <type_traits>
+
 #include "si_kv_common.h"
 
 namespace si {
@@ -141,6 +143,28 @@ struct AttnCfg {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses
+// (lgkmcnt(0)) but, unlike __syncthreads(), not for its global loads, so
+// prefetches stay in flight across it. The signal fences keep the compiler
+// from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int SDT>
+__device__ __forceinline__ uint32_t load_scale_bits(const void* p, int64_t i) {
+  if (SDT == SI_DT_F32) return reinterpret_cast<const uint32_t*>(p)[i];
+  return reinterpret_cast<const uint16_t*>(p)[i];
+}
+template <int SDT>
+__device__ __forceinline__ float scale_from_bits(uint32_t b) {
+  if (SDT == SI_DT_F32) return __builtin_bit_cast(float, b);
+  return SDT == SI_DT_F16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t w) { return __builtin_bit_cast(h2, w); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
@@ -212,9 +236,10 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   constexpr int DPT = C::DPT, RW = C::RW > 0 ? C::RW : 1;
   constexpr int VP = C::VPITCH;
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[BN][D + KPAD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[D][VP];
-  __shared__ __attribute__((aligned(16))) float ksc[BN];
+  // Two tile buffers: tile t+1 is decoded into one while tile t is multiplied from the other.
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[2][BN][D + KPAD];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D][VP];
+  __shared__ __attribute__((aligned(16))) float ksc[2][BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -255,53 +280,60 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   const int n_ev = cnt[4];
   const int T = tstart[4];
   const int32_t* lh = lists + h * cap;
-  auto tile_prec = [&](int tt) {
-    return tt < tstart[1] ? 0 : tt < tstart[2] ? 1 : tt < tstart[3] ? 2 : 3;
-  };
   auto tile_valid = [&](int tt, int p) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
 
   // Decode-stage coordinates: keys 4*kg .. 4*kg+3 of the tile, dims d0 .. d0+DPT-1.
   const int kg = tid / C::DGN;
   const int dg = tid % C::DGN;
   const int d0 = dg * DPT;
+  const int ngrp = (int)(D / g);       // int4 groups per row
+  const int my_grp = d0 / (int)g;      // this thread's group (DPT values never straddle one)
 
   int4 sl = make_int4(0, 0, 0, 0);  // slots of the next tile to fetch
   int4 sl_data = sl;                 // slots of the tile held in rk / rv
   uint32_t rk[4][RW], rv[4][RW];
-  float sk[4], sv[4];
+  uint32_t skb[4], svb[4];  // raw scale bits, converted at decode time
 
+  // Tiles are processed in precision phases (the list regions): every load
+  // and decode below is specialised for the phase's precision P, so no branch
+  // merges registers that still have loads in flight. Prefetches are
+  // unconditional: indices past the phase's last tile are clamped to it (a
+  // harmless re-read).
+  int t_last = 0;  // last tile of the current phase
   auto fetch_slots = [&](int tt) {
+    tt = min(tt, t_last);
     sl = *reinterpret_cast<const int4*>(lh + (int64_t)tt * BN + 4 * kg);
   };
   // Raw loads of the tile's rows into registers (fp32 tiles are read at decode time).
-  auto fetch_data = [&](int tt) {
-    const int p = __builtin_amdgcn_readfirstlane(tile_prec(tt));
-    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, p));
+  auto fetch_data = [&](auto PC, int tt) {
+    constexpr int P = decltype(PC)::value;
+    tt = min(tt, t_last);
+    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
     sl_data = sl;
     const int sl4[4] = {sl.x, sl.y, sl.z, sl.w};
+    if constexpr (P == SI_PREC_FP32) return;  // read at decode time
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int w = 0; w < RW; ++w) rk[i][w] = rv[i][w] = 0u;
-      sk[i] = sv[i] = 0.0f;
-      if (4 * kg + i >= nv || p == SI_PREC_FP32) continue;
-      const int64_t row = (int64_t)sl4[i] * B + b;
-      if (p == SI_PREC_FP16) {
+      // Keys past the tile's valid count read row 0 of the same (non-empty)
+      // bucket: their scores are masked to -inf, so they contribute nothing.
+      const int sli = 4 * kg + i < nv ? sl4[i] : 0;
+      const int64_t row = (int64_t)sli * B + b;
+      if constexpr (P == SI_PREC_FP16) {
         load_raw<2 * DPT>(reinterpret_cast<const uint16_t*>(bk.p[4]) + row * D + d0, rk[i]);
         load_raw<2 * DPT>(reinterpret_cast<const uint16_t*>(bk.p[5]) + row * D + d0, rv[i]);
-      } else if (p == SI_PREC_INT8) {
+      } else if constexpr (P == SI_PREC_INT8) {
         load_raw<DPT>(reinterpret_cast<const int8_t*>(bk.p[8]) + row * D + d0, rk[i]);
         load_raw<DPT>(reinterpret_cast<const int8_t*>(bk.p[9]) + row * D + d0, rv[i]);
-        sk[i] = load_scale<SDT>(bk.p[10], row);
-        sv[i] = load_scale<SDT>(bk.p[11], row);
-      } else {
+        skb[i] = load_scale_bits<SDT>(bk.p[10], row);
+        svb[i] = load_scale_bits<SDT>(bk.p[11], row);
+      } else if constexpr (P == SI_PREC_INT4) {
         const int64_t rb = B * D / 2;  // bytes of one int4 entry row
-        const int64_t off = sl4[i] * rb + (b * D + d0) / 2;
+        const int64_t off = sli * rb + (b * D + d0) / 2;
         load_raw<DPT / 2>(reinterpret_cast<const uint8_t*>(bk.p[12]) + off, rk[i]);
         load_raw<DPT / 2>(reinterpret_cast<const uint8_t*>(bk.p[13]) + off, rv[i]);
-        const int64_t si = row * (D / g) + d0 / g;
-        sk[i] = load_scale<SDT>(bk.p[14], si);
-        sv[i] = load_scale<SDT>(bk.p[15], si);
+        const int64_t si = row * ngrp + my_grp;
+        skb[i] = load_scale_bits<SDT>(bk.p[14], si);
+        svb[i] = load_scale_bits<SDT>(bk.p[15], si);
       }
     }
   };
@@ -314,123 +346,96 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
-  if (T > 0) {
-    fetch_slots(0);
-    fetch_data(0);
-    if (T > 1) fetch_slots(1);
-  }
-  for (int tt = 0; tt < T; ++tt) {
-    const int p = __builtin_amdgcn_readfirstlane(tile_prec(tt));  // block-uniform
-    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, p));
-    // ---- decode the tile into LDS ----
-    __syncthreads();  // the previous tile's MFMAs are done with Ks / Vt / ksc
+  // Decode tile tt (its rows are in rk / rv) into LDS buffer buf.
+  auto decode_tile = [&](auto PC, int tt, int buf) {
+    constexpr int P = decltype(PC)::value;
+    constexpr int p = P;
+    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
     {
-      uint32_t vt[DPT][2];  // V^T words: [e][0] = keys 0,1, [e][1] = keys 2,3 of dim d0 + e
-      auto put_k = [&](int i, const uint32_t* w) {
-        if constexpr (DPT == 8) {
-          *reinterpret_cast<uint4*>(&Ks[4 * kg + i][d0]) = make_uint4(w[0], w[1], w[2], w[3]);
-        } else if constexpr (DPT == 4) {
-          *reinterpret_cast<uint2*>(&Ks[4 * kg + i][d0]) = make_uint2(w[0], w[1]);
-        } else {
-          *reinterpret_cast<uint32_t*>(&Ks[4 * kg + i][d0]) = w[0];
-        }
-      };
-      auto put_v = [&](int i, int e, _Float16 x) {
-        const uint32_t hx = __builtin_bit_cast(uint16_t, x);
-        uint32_t& w = vt[e][i >> 1];
-        w = (i & 1) ? ((w & 0xffffu) | (hx << 16)) : ((w & 0xffff0000u) | hx);
-      };
-      if (p == SI_PREC_FP16) {
+      // The prefetched registers are first read here: nothing computed from
+      // them may move earlier (that would wait for the loads in flight).
 #pragma unroll
-        for (int i = 0; i < 4; ++i) put_k(i, rk[i]);
+      for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int w = 0; w < RW; ++w) {
-          vt[2 * w][0] = __builtin_amdgcn_perm(rv[1][w], rv[0][w], 0x05040100u);
-          vt[2 * w][1] = __builtin_amdgcn_perm(rv[3][w], rv[2][w], 0x05040100u);
-          vt[2 * w + 1][0] = __builtin_amdgcn_perm(rv[1][w], rv[0][w], 0x07060302u);
-          vt[2 * w + 1][1] = __builtin_amdgcn_perm(rv[3][w], rv[2][w], 0x07060302u);
-        }
-      } else if (p == SI_PREC_INT8) {
+        for (int x = 0; x < RW; ++x) asm volatile("" : "+v"(rk[i][x]), "+v"(rv[i][x]));
+        asm volatile("" : "+v"(skb[i]), "+v"(svb[i]));
+      }
+      float sk[4], sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sk[i] = scale_from_bits<SDT>(skb[i]);
+        sv[i] = scale_from_bits<SDT>(svb[i]);
+      }
+      // Per key i: fp16 pair words of K (kw) and V (vw), dims (2x, 2x+1).
+      uint32_t kw[4][RW], vw[4][RW];
+      if constexpr (P == SI_PREC_FP16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int x = 0; x < RW; ++x) {
+            kw[i][x] = rk[i][x];
+            vw[i][x] = rv[i][x];
+          }
+      } else if constexpr (P == SI_PREC_INT8) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // K keeps the integer values (exact in fp16); the scale multiplies the score.
-          uint32_t w[RW];
+          uint32_t unused;
+          if constexpr (DPT >= 4) {
 #pragma unroll
-          for (int x = 0; x < DPT / 4; ++x) i8x4_to_h(rk[i][x], w[2 * x], w[2 * x + 1]);
-          if constexpr (DPT == 2) {
-            uint32_t unused;
-            i8x4_to_h(rk[i][0], w[0], unused);
+            for (int x = 0; x < DPT / 4; ++x) {
+              i8x4_to_h(rk[i][x], kw[i][2 * x], kw[i][2 * x + 1]);
+              i8x4_to_h(rv[i][x], vw[i][2 * x], vw[i][2 * x + 1]);
+            }
+          } else {
+            i8x4_to_h(rk[i][0], kw[i][0], unused);
+            i8x4_to_h(rv[i][0], vw[i][0], unused);
           }
-          put_k(i, w);
           // V: float(q) * float(s) rounded to fp16
           const _Float16 hs = exact_h(sv[i], 128.0f);
           if (hs != (_Float16)0.0f) {
             const h2 s2 = {hs, hs};
-            uint32_t q[RW];
 #pragma unroll
-            for (int x = 0; x < DPT / 4; ++x) i8x4_to_h(rv[i][x], q[2 * x], q[2 * x + 1]);
-            if constexpr (DPT == 2) {
-              uint32_t unused;
-              i8x4_to_h(rv[i][0], q[0], unused);
-            }
-#pragma unroll
-            for (int x = 0; x < RW; ++x) {
-              const h2 v = as_h2(q[x]) * s2;
-              put_v(i, 2 * x, v[0]);
-              put_v(i, 2 * x + 1, v[1]);
-            }
+            for (int x = 0; x < RW; ++x) vw[i][x] = as_u32(as_h2(vw[i][x]) * s2);
           } else {
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) {
-              const float qv = (float)(int8_t)((rv[i][e >> 2] >> (8 * (e & 3))) & 0xffu);
-              put_v(i, e, (_Float16)(qv * sv[i]));
+            for (int x = 0; x < RW; ++x) {
+              const h2 q = as_h2(vw[i][x]);
+              vw[i][x] = pack_h2((_Float16)((float)q[0] * sv[i]), (_Float16)((float)q[1] * sv[i]));
             }
           }
         }
-      } else if (p == SI_PREC_INT4) {
+      } else if constexpr (P == SI_PREC_INT4) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // float(q) * float(s) rounded to fp16, for K and V
-          const _Float16 hk = exact_h(sk[i], 8.0f), hv = exact_h(sv[i], 8.0f);
-          uint32_t w[RW];
           if constexpr (DPT >= 4) {
 #pragma unroll
             for (int x = 0; x < DPT / 4; ++x) {
-              uint32_t qlo, qhi;
-              i4x4_to_h(rk[i][0] >> (16 * x), qlo, qhi);
-              if (hk != (_Float16)0.0f) {
-                const h2 s2 = {hk, hk};
-                w[2 * x] = as_u32(as_h2(qlo) * s2);
-                w[2 * x + 1] = as_u32(as_h2(qhi) * s2);
-              } else {
-                const h2 a = as_h2(qlo), c = as_h2(qhi);
-                w[2 * x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
-                w[2 * x + 1] = pack_h2((_Float16)((float)c[0] * sk[i]), (_Float16)((float)c[1] * sk[i]));
-              }
-              i4x4_to_h(rv[i][0] >> (16 * x), qlo, qhi);
-              const h2 a = as_h2(qlo), c = as_h2(qhi);
-              if (hv != (_Float16)0.0f) {
-                const h2 s2 = {hv, hv};
-                const h2 va = a * s2, vc = c * s2;
-                put_v(i, 4 * x + 0, va[0]);
-                put_v(i, 4 * x + 1, va[1]);
-                put_v(i, 4 * x + 2, vc[0]);
-                put_v(i, 4 * x + 3, vc[1]);
-              } else {
-                put_v(i, 4 * x + 0, (_Float16)((float)a[0] * sv[i]));
-                put_v(i, 4 * x + 1, (_Float16)((float)a[1] * sv[i]));
-                put_v(i, 4 * x + 2, (_Float16)((float)c[0] * sv[i]));
-                put_v(i, 4 * x + 3, (_Float16)((float)c[1] * sv[i]));
-              }
+              i4x4_to_h(rk[i][0] >> (16 * x), kw[i][2 * x], kw[i][2 * x + 1]);
+              i4x4_to_h(rv[i][0] >> (16 * x), vw[i][2 * x], vw[i][2 * x + 1]);
             }
           } else {
             const uint32_t kb = rk[i][0] & 0xffu, vb = rv[i][0] & 0xffu;
-            w[0] = pack_h2((_Float16)((float)((int)(kb >> 4) - 8) * sk[i]),
-                           (_Float16)((float)((int)(kb & 0xfu) - 8) * sk[i]));
-            put_v(i, 0, (_Float16)((float)((int)(vb >> 4) - 8) * sv[i]));
-            put_v(i, 1, (_Float16)((float)((int)(vb & 0xfu) - 8) * sv[i]));
+            kw[i][0] = pack_h2((_Float16)(float)((int)(kb >> 4) - 8), (_Float16)(float)((int)(kb & 0xfu) - 8));
+            vw[i][0] = pack_h2((_Float16)(float)((int)(vb >> 4) - 8), (_Float16)(float)((int)(vb & 0xfu) - 8));
           }
-          put_k(i, w);
+          // float(q) * float(s) rounded to fp16, for K and V
+          const _Float16 hk = exact_h(sk[i], 8.0f), hv = exact_h(sv[i], 8.0f);
+          if (hk != (_Float16)0.0f && hv != (_Float16)0.0f) {
+            const h2 k2 = {hk, hk}, v2 = {hv, hv};
+#pragma unroll
+            for (int x = 0; x < RW; ++x) {
+              kw[i][x] = as_u32(as_h2(kw[i][x]) * k2);
+              vw[i][x] = as_u32(as_h2(vw[i][x]) * v2);
+            }
+          } else {
+#pragma unroll
+            for (int x = 0; x < RW; ++x) {
+              const h2 a = as_h2(kw[i][x]), c = as_h2(vw[i][x]);
+              kw[i][x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
+              vw[i][x] = pack_h2((_Float16)((float)c[0] * sv[i]), (_Float16)((float)c[1] * sv[i]));
+            }
+          }
         }
       } else {  // fp32 bucket rows, read here
         const int sl4[4] = {sl_data.x, sl_data.y, sl_data.z, sl_data.w};
@@ -449,50 +454,78 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
               vx[e] = vp[e];
             }
           }
-          uint32_t w[RW];
 #pragma unroll
-          for (int e = 0; e < DPT; e += 2) w[e >> 1] = pack_h2((_Float16)kx[e], (_Float16)kx[e + 1]);
-          put_k(i, w);
+          for (int x = 0; x < RW; ++x) {
+            kw[i][x] = pack_h2((_Float16)kx[2 * x], (_Float16)kx[2 * x + 1]);
+            vw[i][x] = pack_h2((_Float16)vx[2 * x], (_Float16)vx[2 * x + 1]);
+          }
+        }
+      }
 #pragma unroll
-          for (int e = 0; e < DPT; ++e) put_v(i, e, (_Float16)vx[e]);
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DPT == 8) {
+          *reinterpret_cast<uint4*>(&Ks[buf][4 * kg + i][d0]) =
+              make_uint4(kw[i][0], kw[i][1], kw[i][2], kw[i][3]);
+        } else if constexpr (DPT == 4) {
+          *reinterpret_cast<uint2*>(&Ks[buf][4 * kg + i][d0]) = make_uint2(kw[i][0], kw[i][1]);
+        } else {
+          *reinterpret_cast<uint32_t*>(&Ks[buf][4 * kg + i][d0]) = kw[i][0];
         }
       }
       if (dg == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ksc[4 * kg + i] = p == SI_PREC_INT8 ? sk[i] : 1.0f;
+        for (int i = 0; i < 4; ++i) ksc[buf][4 * kg + i] = p == SI_PREC_INT8 ? sk[i] : 1.0f;
       }
-      // V^T rows d0 + e hold keys 4*kg .. 4*kg+3 (8 bytes).
+      // V^T rows d0 + e hold keys 4*kg .. 4*kg+3 (8 bytes): transpose the pair words.
 #pragma unroll
-      for (int e = 0; e < DPT; ++e)
-        *reinterpret_cast<uint2*>(&Vt[d0 + e][4 * kg]) = make_uint2(vt[e][0], vt[e][1]);
+      for (int x = 0; x < RW; ++x) {
+        *reinterpret_cast<uint2*>(&Vt[buf][d0 + 2 * x][4 * kg]) =
+            make_uint2(__builtin_amdgcn_perm(vw[1][x], vw[0][x], 0x05040100u),
+                       __builtin_amdgcn_perm(vw[3][x], vw[2][x], 0x05040100u));
+        *reinterpret_cast<uint2*>(&Vt[buf][d0 + 2 * x + 1][4 * kg]) =
+            make_uint2(__builtin_amdgcn_perm(vw[1][x], vw[0][x], 0x07060302u),
+                       __builtin_amdgcn_perm(vw[3][x], vw[2][x], 0x07060302u));
+      }
     }
-    __syncthreads();
-    // ---- prefetch: rows of the next tile, slots of the one after ----
-    if (tt + 1 < T) {
-      fetch_data(tt + 1);
-      if (tt + 2 < T) fetch_slots(tt + 2);
-    }
+  };
 
+  // S^T = K Q^T, online softmax and O^T += V^T P^T for tile tt in buffer buf.
+  auto compute_tile = [&](auto PC, int tt, int buf) {
+    constexpr int P = decltype(PC)::value;
+    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
     // ---- S^T = K Q^T for the tile's 64 keys ----
+    // K fragments of k-step ks+1 are read while the MFMAs of k-step ks run.
     v16f sacc[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.0f;
+    {
+      v8h ka[2][2];
+      auto load_k = [&](int ks, v8h* a) {
+        a[0] = *reinterpret_cast<const v8h*>(&Ks[buf][col][ks * 16 + 8 * grp]);
+        a[1] = *reinterpret_cast<const v8h*>(&Ks[buf][32 + col][ks * 16 + 8 * grp]);
+      };
+      load_k(0, ka[0]);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const v8h a = *reinterpret_cast<const v8h*>(&Ks[kb * 32 + col][ks * 16 + 8 * grp]);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], sacc[kb], 0, 0, 0);
+        if (ks + 1 < KS) load_k(ks + 1, ka[(ks + 1) & 1]);
+        sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][0], qf[ks], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][1], qf[ks], sacc[1], 0, 0, 0);
+        if (ks + 1 < KS) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two reads of ks+1
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // then the two MFMAs of ks
+        }
       }
     }
 
     // ---- online softmax (log2 domain; Q carries sm_scale * log2(e)) ----
-    if (p == SI_PREC_INT8) {
+    if constexpr (P == SI_PREC_INT8) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 f = *reinterpret_cast<const float4*>(&ksc[kb * 32 + 8 * q4 + 4 * grp]);
+          const float4 f = *reinterpret_cast<const float4*>(&ksc[buf][kb * 32 + 8 * q4 + 4 * grp]);
           sacc[kb][4 * q4 + 0] *= f.x;
           sacc[kb][4 * q4 + 1] *= f.y;
           sacc[kb][4 * q4 + 2] *= f.z;
@@ -507,11 +540,12 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         for (int r = 0; r < 16; ++r)
           if (kb * 32 + 8 * (r >> 2) + 4 * grp + (r & 3) >= nv) sacc[kb][r] = -INFINITY;
     }
-    float tmax = -INFINITY;
+    float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[kb][r]);
+      for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], sacc[kb][r]);
+    float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const bool raise = tmax > m_run + 8.0f;
     if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -524,7 +558,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
       m_run = m_new;
     }
-    float psum = 0.0f;
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -532,29 +566,71 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         // v_exp_f32: arguments are <= 8 here; results below 2^-126 flush to 0
         const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_run);
         sacc[kb][r] = pr;
-        psum += pr;
+        ps[r & 3] += pr;
       }
     }
+    const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
     l_run += psum + __shfl_xor(psum, 32, 64);
 
     // ---- O^T += V^T P^T over four 16-key chunks ----
+    // V^T fragments of chunk c+1 are read while the MFMAs of chunk c run.
+    {
+      v8h va[2][DB];
+      auto load_v = [&](int c, v8h* a) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int kb = c >> 1;
-      const int hc = c & 1;
-      v8h pb;
+        for (int db = 0; db < DB; ++db) {
+          const _Float16* vrow = &Vt[buf][db * 32 + col][c * 16 + 4 * grp];
+          const v4h lo = *reinterpret_cast<const v4h*>(vrow);
+          const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
+          a[db] = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      };
+      load_v(0, va[0]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pb[i] = (_Float16)sacc[kb][8 * hc + i];
+      for (int c = 0; c < 4; ++c) {
+        if (c + 1 < 4) load_v(c + 1, va[(c + 1) & 1]);
+        const int kb = c >> 1;
+        const int hc = c & 1;
+        v8h pb;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const _Float16* vrow = &Vt[db * 32 + col][c * 16 + 4 * grp];
-        const v4h lo = *reinterpret_cast<const v4h*>(vrow);
-        const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
-        const v8h a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[db], 0, 0, 0);
+        for (int i = 0; i < 8; ++i) pb[i] = (_Float16)sacc[kb][8 * hc + i];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c & 1][db], pb, o[db], 0, 0, 0);
       }
     }
-  }
+  };
+
+  int buf = 0;
+  auto run_phase = [&](auto PC) {
+    constexpr int P = decltype(PC)::value;
+    const int t0 = tstart[P], t1 = tstart[P + 1];
+    if (t0 >= t1) return;
+    t_last = t1 - 1;
+    fetch_slots(t0);
+    fetch_data(PC, t0);
+    fetch_slots(t0 + 1);
+    decode_tile(PC, t0, buf);
+    fetch_data(PC, t0 + 1);
+    fetch_slots(t0 + 2);
+    lds_barrier();
+    for (int tt = t0; tt < t1; ++tt) {
+      compute_tile(PC, tt, buf);
+      // Decode the next tile into the other buffer (after the phase's last
+      // tile: a clamped copy nobody reads), then prefetch.
+      decode_tile(PC, min(tt + 1, t_last), buf ^ 1);
+      fetch_data(PC, tt + 2);
+      fetch_slots(tt + 3);
+      // Buffer buf ^ 1 is complete and every wave is done with buffer buf.
+      lds_barrier();
+      buf ^= 1;
+    }
+    // The phase's last decode (a clamped copy) went into buf; nothing reads it.
+  };
+  run_phase(std::integral_constant<int, SI_PREC_FP32>{});
+  run_phase(std::integral_constant<int, SI_PREC_FP16>{});
+  run_phase(std::integral_constant<int, SI_PREC_INT8>{});
+  run_phase(std::integral_constant<int, SI_PREC_INT4>{});
 
   // Evicted / absent keys: score 0, value 0.
   if (n_ev > 0) {
