@@ -291,6 +291,15 @@ __device__ __forceinline__ void wait_cnt() {
   __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (LGKM << 8));
 }
 
+// s_barrier without the fence of __syncthreads() (which would also wait for
+// every copy in flight). The signal fences keep the compiler from moving
+// memory accesses across it; callers wait for what must be complete first.
+__device__ __forceinline__ void bare_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Wait until at most n k-tiles of this wave's copies are still in flight
 // (n <= S - 2 <= 2), with every LDS read of this wave complete.
 template <int LPT, int S>
@@ -433,7 +442,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
   if (nk > 0) {
     for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
     wait_tiles<LPT, S>(min(nk - 1, S - 2));
-    __builtin_amdgcn_s_barrier();
+    bare_barrier();
     load_frags(lds, 0, af[0], bf[0]);
   }
   for (int t = 0; t < nk; ++t) {
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
         // below): after the last k-tile it waits for nothing and reads a
         // stale stage whose fragments are never used.
         wait_tiles<LPT, S>(min(nk - 2 - t, S - 2));
-        __builtin_amdgcn_s_barrier();
+        bare_barrier();
         load_frags(lds + ((t + 1) % S) * STAGE, 0, af[cur ^ 1], bf[cur ^ 1]);
       }
 #pragma unroll
