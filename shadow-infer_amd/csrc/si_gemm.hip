@@ -301,13 +301,16 @@ __device__ __forceinline__ void bare_barrier() {
 }
 
 // Wait until at most n k-tiles of this wave's copies are still in flight
-// (n <= S - 2 <= 2), with every LDS read of this wave complete.
-template <int LPT, int S>
+// (0 <= n <= S - 2), with every LDS read of this wave complete.
+template <int LPT, int S, int I = S - 2>
 __device__ __forceinline__ void wait_tiles(int n) {
-  static_assert(S >= 2 && S <= 4, "stage count");
-  if (S == 4 && n >= 2) wait_cnt<(S == 4 ? 2 * LPT : 0), 0>();
-  else if (S >= 3 && n >= 1) wait_cnt<(S >= 3 ? LPT : 0), 0>();
-  else wait_cnt<0, 0>();
+  static_assert(S >= 2 && I * LPT <= 63, "vmcnt holds at most 63 outstanding loads");
+  if constexpr (I <= 0) {
+    wait_cnt<0, 0>();
+  } else {
+    if (n >= I) wait_cnt<I * LPT, 0>();
+    else wait_tiles<LPT, S, I - 1>(n);
+  }
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs. Renumber them so
@@ -623,6 +626,118 @@ __global__ __launch_bounds__(256) void gemm_skinny(const int8_t* __restrict__ A,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Weight-streaming kernel (M <= 16*MF, bound by reading the weight once): a
+// block owns 16*NF output columns and its NW waves split K into NW ranges;
+// their int32 partial sums are added in LDS, so nothing but the output leaves
+// the block. Fragments use the 16x16x64 layout (lane l holds row or column
+// l%16 and k bytes 16*(l/16) .. +15 of a 64-byte k step) and are loaded
+// straight into registers in batches of U k steps, two batches in flight:
+// one is multiplied while the next streams in.
+// Requires K % 64 == 0.
+// ---------------------------------------------------------------------------
+template <int MF, int NF, int NW, int U, int EPI>
+__global__ __launch_bounds__(64 * NW) void gemm_stream(const int8_t* __restrict__ A,
+                                                       const int8_t* __restrict__ B, int M, int N,
+                                                       int K, int32_t* __restrict__ C, EpiArgs ep) {
+  constexpr int RP = 16 * NF + 4;  // LDS pitch (words) of a partial-sum row; rows 4 apart hit other banks
+  constexpr int PART = MF * 16 * RP;
+  __shared__ int32_t red[NW * PART];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NF;
+  const int ksteps = K / 64;
+  const int q = (ksteps + NW - 1) / NW;
+  const int s0 = min(w * q, ksteps);
+  const int s1 = min(s0 + q, ksteps);
+  const int8_t* bp[NF];
+  const int8_t* ap[MF];
+#pragma unroll
+  for (int j = 0; j < NF; ++j) bp[j] = B + (int64_t)min(n0 + 16 * j + c, N - 1) * K + 16 * g;
+#pragma unroll
+  for (int i = 0; i < MF; ++i) ap[i] = A + (int64_t)min(16 * i + c, M - 1) * K + 16 * g;
+
+  v4i acc[MF][NF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int j = 0; j < NF; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  v4i b0[U][NF], a0[U][MF], b1[U][NF], a1[U][MF];
+  auto load = [&](v4i (&bb)[U][NF], v4i (&aa)[U][MF], int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int j = 0; j < NF; ++j)
+        bb[u][j] = *reinterpret_cast<const v4i*>(bp[j] + 64 * (s + u));
+#pragma unroll
+      for (int i = 0; i < MF; ++i) aa[u][i] = *reinterpret_cast<const v4i*>(ap[i] + 64 * (s + u));
+    }
+  };
+  auto mul = [&](v4i (&bb)[U][NF], v4i (&aa)[U][MF]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[u][i], bb[u][j], acc[i][j], 0, 0, 0);
+  };
+  const int nb = (s1 - s0) / U;  // whole batches of this wave
+  if (nb > 0) {
+    load(b0, a0, s0);
+    int bi = 0;
+    for (; bi + 2 < nb; bi += 2) {
+      load(b1, a1, s0 + (bi + 1) * U);
+      mul(b0, a0);
+      load(b0, a0, s0 + (bi + 2) * U);
+      mul(b1, a1);
+    }
+    if (bi + 1 < nb) {  // two batches left: bi (in b0) and bi + 1
+      load(b1, a1, s0 + (bi + 1) * U);
+      mul(b0, a0);
+      mul(b1, a1);
+    } else {
+      mul(b0, a0);
+    }
+  }
+  for (int s = s0 + nb * U; s < s1; ++s) {
+    v4i bb[1][NF], aa[1][MF];
+#pragma unroll
+    for (int j = 0; j < NF; ++j) bb[0][j] = *reinterpret_cast<const v4i*>(bp[j] + 64 * s);
+#pragma unroll
+    for (int i = 0; i < MF; ++i) aa[0][i] = *reinterpret_cast<const v4i*>(ap[i] + 64 * s);
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[0][i], bb[0][j], acc[i][j], 0, 0, 0);
+  }
+
+  // Partial sums to LDS: accumulator register r of fragment (i, j) holds row
+  // 16i + 4(lane/16) + r, column 16j + lane%16.
+  int32_t* mine = red + w * PART;
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int j = 0; j < NF; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mine[(16 * i + 4 * g + r) * RP + 16 * j + c] = acc[i][j][r];
+  __syncthreads();
+  constexpr int W = 16 * NF;
+  for (int e = threadIdx.x; e < MF * 16 * W; e += 64 * NW) {
+    const int m = e / W;
+    const int nn = e % W;
+    const int n = n0 + nn;
+    if (m >= M || n >= N) continue;
+    int32_t v = 0;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) v += red[x * PART + m * RP + nn];
+    epi_store<EPI>(ep, C, M, N, m, n, v, 0);
+  }
+}
+
 // Sum split-K partials (exact integer adds) and store int32 or dequantized.
 __global__ __launch_bounds__(256) void gemm_finalize(const int32_t* __restrict__ partial,
                                                      int splits, int64_t M, int64_t N,
@@ -671,7 +786,8 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             K_DMA_256x64 = 11, K_DMA_256x128_K128 = 12,
             // eight waves per block (two per SIMD)
             K_DMA8_256x256 = 13, K_DMA8_256x256_K128 = 14, K_DMA8_256x192_K128 = 15,
-            K_DMA8_256x128 = 16, K_DMA8_128x256 = 17 };
+            K_DMA8_256x128 = 16, K_DMA8_128x256 = 17,
+            K_STREAM_N64 = 25, K_STREAM_N64_W8 = 27 };
 
 struct Plan {
   int kind;
@@ -698,8 +814,8 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   int kind;
   if (forced_kind() >= 0) {
     kind = forced_kind();
-  } else if (M <= 16 && K % 64 == 0) {
-    kind = K_SKINNY;  // 4096 x 11008, M = 16: 22 us (DMA 128x128: 23 us)
+  } else if (M <= 32 && K % 64 == 0) {
+    kind = K_STREAM_N64;  // 4096 x 11008: M = 1 13 us, M = 16 14 us, M = 32 16 us
   } else if (M <= 384 && K % 128 == 0) {
     kind = K_DMA_128x128;  // M = 64: 21 us, M = 256: 25 us
   } else if (M <= 640 && K % 128 == 0) {
@@ -713,6 +829,15 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   }
   if (kind == K_SKINNY) {
     if (M > 64 || K % 64 != 0) kind = K_TILE_128x128;
+  }
+  if (kind == K_STREAM_N64 || kind == K_STREAM_N64_W8) {
+    if (M > 64 || K % 64 != 0) {
+      kind = K_TILE_128x128;
+    } else {
+      p.kind = kind;
+      p.mf = (int)ceil_div(M, 16);
+      return p;
+    }
   }
   p.kind = kind;
   if (kind == K_SKINNY) {
@@ -794,10 +919,30 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
 #undef SI_DMA
 }
 
+template <int MF, int EPI>
+void launch_stream(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
+                   const EpiArgs& ep, hipStream_t st) {
+#define SI_STREAM(NF_, NW_, U_)                                                           \
+  gemm_stream<MF, NF_, NW_, U_, EPI><<<dim3((unsigned)ceil_div(N, 16 * NF_)), dim3(64 * NW_), 0, st>>>( \
+      a, b, M, N, K, c, ep)
+  if (p.kind == K_STREAM_N64_W8) SI_STREAM(4, 8, 2);
+  else SI_STREAM(4, 4, 4);
+#undef SI_STREAM
+}
+
 template <int EPI>
 void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
             const EpiArgs& ep, hipStream_t st) {
   const dim3 block(256);
+  if (p.kind == K_STREAM_N64 || p.kind == K_STREAM_N64_W8) {
+    switch (p.mf) {
+      case 1: launch_stream<1, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 2: launch_stream<2, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 3: launch_stream<3, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      default: launch_stream<4, EPI>(p, a, b, M, N, K, c, ep, st);
+    }
+    return;
+  }
   if (p.kind == K_SKINNY) {
     const dim3 grid((unsigned)ceil_div(ceil_div(N, 16), 4), (unsigned)p.splits);
     switch (p.mf) {
