@@ -341,6 +341,83 @@ __device__ __forceinline__ void store8(void* out, int64_t idx, const float* o) {
   }
 }
 
+// Stores one 32-row band (FN fragments of 32x32 int32 accumulators) of a
+// wave through its own LDS staging area of 16 x (32*FN + 8) words, in two
+// passes of 16 rows, as 16-byte row stores (int32, or dequantized when EPI
+// is EPI_DEQUANT + 16 * output dtype). Accumulator register r of a fragment
+// holds row 8*(r/4) + 4*(lane/32) + r%4, column lane%32, so registers
+// [8h, 8h+8) hold rows 16h .. 16h+15.
+template <int FN, int EPI>
+__device__ __forceinline__ void store_frag_row(const v16i* acc, int m_base, int n_base, int32_t* stg,
+                                               int lane, int M, int N, int32_t* dst,
+                                               const EpiArgs& ep) {
+  constexpr int TN = 32 * FN;
+  constexpr int EP = TN + 8;  // staging pitch in words (rows r and r+4 on other banks)
+  constexpr int CH = TN / 8;  // 8-wide chunks per staged row
+  constexpr int KIND = EPI & 15;
+  constexpr int ODT = EPI >> 4;
+  const int col = lane & 31;
+  const int rq = (lane >> 5) * 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 8 * h; r < 8 * h + 8; ++r)
+        stg[(8 * (r >> 2) - 16 * h + rq + (r & 3)) * EP + j * 32 + col] = acc[j][r];
+    wait_cnt<63, 0>();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = lane; c < 16 * CH; c += 64) {
+      const int row = c / CH;
+      const int ch = c % CH;
+      const int m = m_base + 16 * h + row;
+      const int n = n_base + ch * 8;
+      if (m >= M || n >= N) continue;
+      const int32_t* sp = stg + row * EP + ch * 8;
+      const v4i lo = *reinterpret_cast<const v4i*>(sp);
+      const v4i hi = *reinterpret_cast<const v4i*>(sp + 4);
+      const int32_t v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const int64_t idx = (int64_t)m * N + n;
+      const bool full = ep.vec && n + 8 <= N;
+      if constexpr (KIND != EPI_DEQUANT) {
+        if (full) {
+          reinterpret_cast<v4i*>(dst + idx)[0] = lo;
+          reinterpret_cast<v4i*>(dst + idx)[1] = hi;
+        } else {
+          for (int e = 0; e < 8 && n + e < N; ++e) dst[idx + e] = v[e];
+        }
+      } else {
+        const float sx = ep.sx[m];
+        float o[8];
+        if (full) {
+          const float4 w0 = reinterpret_cast<const float4*>(ep.sw + n)[0];
+          const float4 w1 = reinterpret_cast<const float4*>(ep.sw + n)[1];
+          const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (float)v[e] * (sx * w[e]);
+          if (ep.bias != nullptr) {
+            const float4 b0 = reinterpret_cast<const float4*>(ep.bias + n)[0];
+            const float4 b1 = reinterpret_cast<const float4*>(ep.bias + n)[1];
+            const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = o[e] + bb[e];
+          }
+          store8<ODT>(ep.out, idx, o);
+        } else {
+          for (int e = 0; e < 8 && n + e < N; ++e) {
+            float x = (float)v[e] * (sx * ep.sw[n + e]);
+            if (ep.bias != nullptr) x = x + ep.bias[n + e];
+            store_out<ODT>(ep.out, idx + e, x);
+          }
+        }
+      }
+    }
+    wait_cnt<63, 0>();
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int S, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restrict__ A,
                                                          const int8_t* __restrict__ B, int M,
@@ -487,76 +564,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
 
   // ------------------------------------------------------------- epilogue
   __syncthreads();  // every wave is done with the stages
-  // Staging in passes of 16 rows: accumulator registers r in [8h, 8h+8) of a
-  // 32x32 fragment hold rows 16h .. 16h+15 (row 8*(r/4) + 4*(lane/32) + r%4).
   int32_t* stg = reinterpret_cast<int32_t*>(lds) + wave * (16 * EP);
-  const int col = lane & 31;
-  const int rq = (lane >> 5) * 4;
-  constexpr int KIND = EPI & 15;
-  constexpr int ODT = EPI >> 4;
-  constexpr int CH = TN / 8;  // 8-wide chunks per staged row
-  int32_t* dst = KIND == EPI_PARTIAL ? ep.partial + (int64_t)split * M * N : Cout;
+  int32_t* dst = (EPI & 15) == EPI_PARTIAL ? ep.partial + (int64_t)split * M * N : Cout;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 8 * h; r < 8 * h + 8; ++r)
-          stg[(8 * (r >> 2) - 16 * h + rq + (r & 3)) * EP + j * 32 + col] = acc[i][j][r];
-      wait_cnt<63, 0>();
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int c = lane; c < 16 * CH; c += 64) {
-        const int row = c / CH;
-        const int ch = c % CH;
-        const int m = m0 + wm * TM + i * 32 + 16 * h + row;
-        const int n = n0 + wn * TN + ch * 8;
-        if (m >= M || n >= N) continue;
-        const int32_t* sp = stg + row * EP + ch * 8;
-        const v4i lo = *reinterpret_cast<const v4i*>(sp);
-        const v4i hi = *reinterpret_cast<const v4i*>(sp + 4);
-        const int32_t v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        const int64_t idx = (int64_t)m * N + n;
-        const bool full = ep.vec && n + 8 <= N;
-        if constexpr (KIND != EPI_DEQUANT) {
-          if (full) {
-            reinterpret_cast<v4i*>(dst + idx)[0] = lo;
-            reinterpret_cast<v4i*>(dst + idx)[1] = hi;
-          } else {
-            for (int e = 0; e < 8 && n + e < N; ++e) dst[idx + e] = v[e];
-          }
-        } else {
-          const float sx = ep.sx[m];
-          float o[8];
-          if (full) {
-            const float4 w0 = reinterpret_cast<const float4*>(ep.sw + n)[0];
-            const float4 w1 = reinterpret_cast<const float4*>(ep.sw + n)[1];
-            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (float)v[e] * (sx * w[e]);
-            if (ep.bias != nullptr) {
-              const float4 b0 = reinterpret_cast<const float4*>(ep.bias + n)[0];
-              const float4 b1 = reinterpret_cast<const float4*>(ep.bias + n)[1];
-              const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-              for (int e = 0; e < 8; ++e) o[e] = o[e] + bb[e];
-            }
-            store8<ODT>(ep.out, idx, o);
-          } else {
-            for (int e = 0; e < 8 && n + e < N; ++e) {
-              float x = (float)v[e] * (sx * ep.sw[n + e]);
-              if (ep.bias != nullptr) x = x + ep.bias[n + e];
-              store_out<ODT>(ep.out, idx + e, x);
-            }
-          }
-        }
-      }
-      wait_cnt<63, 0>();
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
+  for (int i = 0; i < FM; ++i)
+    store_frag_row<FN, EPI>(acc[i], m0 + wm * TM + i * 32, n0 + wn * TN, stg, lane, M, N, dst, ep);
 }
 
 // ---------------------------------------------------------------------------
