@@ -226,6 +226,40 @@ int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64
                            void* out, void* workspace, size_t workspace_bytes,
                            si_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Rate-distortion admission                                               */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces kv_sensitivity (shadowinfer/shadowkv/rd_allocator.py:47-61):
+ * k, v [B, H, S, D] in `dtype`; out [S, H] in `dtype`,
+ * out[t, h] = (amax_{b,d}|k|^2 + amax_{b,d}|v|^2) / 2 with every operation
+ * rounded to `dtype` (NaN propagates). */
+int si_kv_sensitivity(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+                      int64_t D, void* out, si_stream_t stream);
+
+/* Bytes of device workspace si_admit_codes needs for n_entries = S * H. */
+size_t si_admit_workspace_bytes(int64_t n_entries);
+
+/* Replaces admit_codes (shadowinfer/shadowkv/rd_allocator.py:190-318) and
+ * predict_codes_bytes (:173-188).
+ * codes, out_codes: int8 [S, H] (token-major; out_codes may not alias codes)
+ * importance      : fp32 [S, H]
+ * sensitivity     : fp32 [S, H], or NULL to rank by importance alone
+ * protected_mask  : uint8 [S, H] (non-zero = never touched), or NULL
+ * sink_tokens     : tokens t < sink_tokens are never touched
+ * budget_bytes    : applied when use_budget != 0 (any value); otherwise the
+ *                   codes are copied and only their bytes are summed
+ * costs           : HOST int64 [5], bytes of one token-head per code
+ *                   (int(entry_bytes(...)), rd_allocator.py:26-44)
+ * result          : device int64 [3]: predicted bytes, newly evicted entries,
+ *                   1 if a code outside 0..4 was seen (then nothing is admitted)
+ * workspace       : 256-byte aligned, si_admit_workspace_bytes(S * H) bytes */
+int si_admit_codes(const int8_t* codes, int8_t* out_codes, int64_t S, int64_t H,
+                   const float* importance, const float* sensitivity,
+                   const uint8_t* protected_mask, int64_t sink_tokens, int64_t budget_bytes,
+                   int use_budget, int allow_eviction, const int64_t* costs, int64_t* result,
+                   void* workspace, size_t workspace_bytes, si_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

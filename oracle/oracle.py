@@ -72,6 +72,7 @@ def lib() -> ctypes.CDLL:
             "or_gemm_i8": [vp, vp, i64, i64, i64, vp],
             "or_int8_epilogue": [vp, vp, vp, vp, i64, i64, vp, i32],
             "or_attention": [vp, vp, vp, i64, i64, i64, i64, ctypes.c_double, vp, vp],
+            "or_kv_sensitivity": [vp, vp, i32, i64, i64, i64, i64, vp],
         }
         for name, args in sig.items():
             fn = getattr(_lib, name)
@@ -560,3 +561,177 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
     work = np.empty(Skv, np.float64)
     lib().or_attention(_p(q), _p(k), _p(v), BH, Sq, Skv, D, sm_scale, _p(out), _p(work))
     return out
+
+
+# --------------------------------------------------------------------------
+# Rate-distortion admission (shadowinfer/shadowkv/rd_allocator.py)
+# --------------------------------------------------------------------------
+
+CODE_NAMES = {0: "fp32", 1: "fp16", 2: "int8", 3: "int4", 4: "evicted"}
+LADDER = {"fp32": "fp16", "fp16": "int8", "int8": "int4"}
+
+
+def entry_bytes(precision: str, batch: int, head_dim: int, group_size: int = 16) -> float:
+    """Stored bytes of one token-head, K + V with scales (rd_allocator.py:26-44)."""
+    p = precision.lower()
+    if p == "evicted":
+        return 0.0
+    if p == "int4":
+        group = group_size if group_size > 0 and head_dim % group_size == 0 else head_dim
+        per_tensor = batch * head_dim / 2.0 + batch * (head_dim // group) * 4
+    elif p == "int8":
+        per_tensor = batch * head_dim + batch * 4
+    elif p == "fp32":
+        per_tensor = batch * head_dim * 4
+    else:
+        per_tensor = batch * head_dim * 2
+    return per_tensor * 2.0
+
+
+def code_costs(batch: int, head_dim: int, group_size: int = 16) -> np.ndarray:
+    """int64 bytes per code 0..4 (rd_allocator.py:180-188, 222-229)."""
+    return np.array([int(entry_bytes(CODE_NAMES[c], batch, head_dim, group_size)) for c in range(5)],
+                    np.int64)
+
+
+def kv_sensitivity(k: np.ndarray, v: np.ndarray, dt: int) -> np.ndarray:
+    """kv_sensitivity (rd_allocator.py:47-61): k, v [B, H, S, D] in dtype ``dt``
+    (fp32 values or fp16/bf16 bits); returns [S, H] in ``dt``."""
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    if k.shape != v.shape:
+        raise ValueError("k and v must have identical shapes")
+    B, H, S, D = k.shape
+    out = np.empty((S, H), _np_dtype(dt))
+    lib().or_kv_sensitivity(_p(k), _p(v), dt, B, H, S, D, _p(out))
+    return out
+
+
+def _score(importance, sensitivity, rd_allocation, S, H):
+    imp = np.asarray(importance, np.float32)[:S, :H]
+    sens = np.asarray(sensitivity, np.float32)[:S, :H]
+    if sens.shape != imp.shape:
+        sens = np.ones_like(imp)
+    return (imp * sens).astype(np.float32) if rd_allocation else imp
+
+
+def admit_codes(codes: np.ndarray, importance, sensitivity, budget_bytes, batch: int,
+                head_dim: int, sink_tokens: int = 0, rd_allocation: bool = True,
+                allow_eviction: bool = False, protected_mask=None,
+                group_size: int = 16) -> Tuple[np.ndarray, int, int]:
+    """Closed-form greedy ladder of admit_codes (rd_allocator.py:190-318):
+    stable ascending argsort of the score, prefix sums of the per-candidate
+    savings, searchsorted for the boundary, partial downgrade of the boundary
+    entry, then the optional eviction prefix."""
+    codes = np.asarray(codes)
+    if codes.ndim != 2:
+        raise ValueError("codes must be 2-D [seq, heads]")
+    out = codes.astype(np.int8).copy()
+    S, H = out.shape
+    flat = out.reshape(-1)
+    costs = code_costs(batch, head_dim, group_size)
+    predicted = int(costs[flat.astype(np.int64)].sum())
+    if budget_bytes is None or budget_bytes < 0:
+        return out, predicted, 0
+    score = _score(importance, sensitivity, rd_allocation, S, H)
+    eligible = np.ones((S, H), bool)
+    if sink_tokens > 0:
+        eligible[: min(int(sink_tokens), S)] = False
+    if protected_mask is not None:
+        eligible &= ~np.asarray(protected_mask, bool)[:S, :H]
+    order = np.argsort(score.reshape(-1), kind="stable")
+    cand = order[eligible.reshape(-1)[order]]
+    if cand.size == 0:
+        return out, predicted, 0
+    deltas = np.array([costs[c] - costs[c + 1] for c in (0, 1, 2)], np.int64)
+
+    if predicted > budget_bytes:
+        excess = predicted - budget_bytes
+        base = flat[cand].astype(np.int64)
+        step1 = np.where(base < 3, deltas[np.minimum(base, 2)], 0)
+        next1 = np.where(base < 3, base + 1, base)
+        step2 = np.where(next1 < 3, deltas[np.minimum(next1, 2)], 0)
+        next2 = np.where(next1 < 3, next1 + 1, next1)
+        step3 = np.where(next2 < 3, deltas[np.minimum(next2, 2)], 0)
+        cum = np.cumsum(step1 + step2 + step3)
+        boundary = min(int(np.searchsorted(cum, excess, side="left")), cand.size)
+        new = base.copy()
+        new[:boundary] = np.where(base[:boundary] != 4, 3, base[:boundary])
+        if boundary < cand.size:
+            remaining = excess - (int(cum[boundary - 1]) if boundary > 0 else 0)
+            if base[boundary] != 4:
+                if remaining <= step1[boundary]:
+                    new[boundary] = next1[boundary]
+                elif remaining <= step1[boundary] + step2[boundary]:
+                    new[boundary] = next2[boundary]
+                else:
+                    new[boundary] = 3
+        flat[cand] = new.astype(np.int8)
+        predicted = int(costs[flat.astype(np.int64)].sum())
+
+    evicted = 0
+    if allow_eviction and predicted > budget_bytes:
+        excess = predicted - budget_bytes
+        cum = np.cumsum(costs[flat[cand].astype(np.int64)])
+        boundary = int(np.searchsorted(cum, excess, side="left"))
+        if boundary >= cand.size:
+            boundary = cand.size - 1
+        target = cand[: boundary + 1]
+        evicted = int((flat[target] != 4).sum())
+        flat[target] = 4
+        predicted = int(costs[flat.astype(np.int64)].sum())
+    return out, predicted, evicted
+
+
+def admit_budget_greedy(importance, sensitivity, precision_map: Dict[int, Dict[int, str]],
+                        budget_bytes, batch: int, head_dim: int, sink_tokens: int = 0,
+                        rd_allocation: bool = True, allow_eviction: bool = False,
+                        protected=None, group_size: int = 16):
+    """The per-candidate greedy loop of admit_budget (rd_allocator.py:66-170),
+    one ladder step at a time: an independent formulation of the same
+    admission, used to pin admit_codes."""
+    result = {int(t): dict(m) for t, m in precision_map.items()}
+
+    def total():
+        return int(sum(entry_bytes(p, batch, head_dim, group_size)
+                       for m in result.values() for p in m.values()))
+
+    if budget_bytes is None or budget_bytes < 0:
+        return result, total(), 0
+    imp = np.asarray(importance, np.float32)
+    S = min(imp.shape[0], max(result.keys(), default=0) + 1)
+    H = min(imp.shape[1] if imp.ndim > 1 else 1, max((len(m) for m in result.values()), default=0))
+    if S <= 0 or H <= 0:
+        return result, total(), 0
+    score = _score(importance, sensitivity, rd_allocation, S, H)
+    protected = frozenset(protected or ())
+    cands = sorted(((float(score[t, h]), t, h) for t in range(S) for h in range(H)
+                    if t >= sink_tokens and (t, h) not in protected), key=lambda c: c[0])
+    predicted = total()
+    i = 0
+    while predicted > budget_bytes and i < len(cands):
+        _, t, h = cands[i]
+        m = result.setdefault(t, {})
+        cur = m.get(h, "fp16")
+        nxt = LADDER.get(cur)
+        if nxt is None:
+            i += 1
+            continue
+        predicted -= int(entry_bytes(cur, batch, head_dim, group_size)
+                         - entry_bytes(nxt, batch, head_dim, group_size))
+        m[h] = nxt
+        if nxt == "int4":
+            i += 1
+    evicted = 0
+    if allow_eviction and predicted > budget_bytes:
+        i = 0
+        while predicted > budget_bytes and i < len(cands):
+            _, t, h = cands[i]
+            m = result.setdefault(t, {})
+            cur = m.get(h, "fp16")
+            if cur != "evicted":
+                predicted -= int(entry_bytes(cur, batch, head_dim, group_size))
+                m[h] = "evicted"
+                evicted += 1
+            i += 1
+    return result, int(predicted), evicted

@@ -290,3 +290,29 @@ void or_attention(const float* q, const float* k, const float* v, int64_t BH, in
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* kv_sensitivity (shadowinfer/shadowkv/rd_allocator.py:47-61)               */
+/*   k_abs = k.abs().amax(dim=(0, -1)); v_abs likewise      [H, S], dtype T   */
+/*   s = (k_abs.square() + v_abs.square()) / 2.0            every op in T     */
+/*   out = s.transpose(0, 1)                                [S, H]            */
+/* k, v [B, H, S, D] in dtype T; out [S, H] in T.                            */
+void or_kv_sensitivity(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                       int64_t S, int64_t D, void* out) {
+  for (int64_t t = 0; t < S; ++t) {
+    for (int64_t h = 0; h < H; ++h) {
+      float ka = 0.0f, va = 0.0f;
+      for (int64_t b = 0; b < B; ++b) {
+        const int64_t row = ((b * H + h) * S + t) * D;
+        for (int64_t d = 0; d < D; ++d) {
+          ka = amax_update(ka, load_elem(k, dtype, row + d));
+          va = amax_update(va, load_elem(v, dtype, row + d));
+        }
+      }
+      const float sk = round_to(ka * ka, dtype);
+      const float sv = round_to(va * va, dtype);
+      const float sum = round_to(sk + sv, dtype);
+      store_elem(out, dtype, t * H + h, sum / 2.0f);
+    }
+  }
+}

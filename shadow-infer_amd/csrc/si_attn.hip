@@ -278,7 +278,6 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     tstart[p + 1] = tstart[p] + (np[p] + BN - 1) / BN;
   }
   const int n_ev = cnt[4];
-  const int T = tstart[4];
   const int32_t* lh = lists + h * cap;
   auto tile_valid = [&](int tt, int p) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
 

@@ -1,8 +1,16 @@
-"""Packed mixed-precision KV cache (PackedKVCache), its precision plan and the
-fused packed-KV attention."""
+"""Packed mixed-precision KV cache (PackedKVCache), its precision plan, the
+rate-distortion admission that chooses the precisions, and the fused
+packed-KV attention."""
 
 from .packed_attention import packed_attention
 from .packed_kv_cache import PackedKVCache
+from .rd_allocator import (
+    admit_budget,
+    admit_codes,
+    entry_bytes,
+    kv_sensitivity,
+    predict_codes_bytes,
+)
 from .precision_plan import (
     CODE_PRECISIONS,
     EVICTED,
@@ -20,7 +28,12 @@ __all__ = [
     "PRECISION_ORDER",
     "PackedKVCache",
     "PrecisionPlan",
+    "admit_budget",
+    "admit_codes",
     "codes_to_map",
+    "entry_bytes",
+    "kv_sensitivity",
     "map_to_codes",
     "packed_attention",
+    "predict_codes_bytes",
 ]

@@ -74,8 +74,11 @@ def test_argument_validation_needs_no_device():
 
 def test_workspace_queries():
     assert _native.size_query("si_attn_workspace_bytes", 32, 8192) >= 32 * 8192 * 4
-    assert _native.size_query("si_gemm_workspace_bytes", 16, 11008, 4096) > 0  # split-K
+    # small M streams the weight with K split inside the block: no partials
+    assert _native.size_query("si_gemm_workspace_bytes", 16, 11008, 4096) == 0
     assert _native.size_query("si_gemm_workspace_bytes", 2048, 11008, 4096) == 0
+    n = 8192 * 32
+    assert _native.size_query("si_admit_workspace_bytes", n) >= 5 * n
     assert _native.size_query("si_int8_linear_workspace_bytes", 16, 4096, 11008) >= 16 * 4096
 
 
