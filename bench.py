@@ -12,11 +12,13 @@ bytes; unpack reads the packed bytes and the codes and writes fp32 K+V
 
 Also reported on the same JSON line: per-kernel times with the roofline of the
 dominant kernel, the INT8 FFN GEMM (4096 x 11008, M in {16, 64, 256, 1024}) in
-TOPS against the int8 MFMA peak, the fused packed-KV attention, and the CPU
-baseline (the oracle on the host, a bounded sample of the same workload).
+TOPS against the int8 MFMA peak, the fused packed-KV attention, the
+rate-distortion admission of one layer (sensitivity proxy + budget solver),
+and the CPU baseline (the oracle on the host, a bounded sample of the same
+workload).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--part all|kv|gemm|attention|calib]
+                       [--part all|kv|gemm|attention|admit|calib]
 """
 
 from __future__ import annotations
@@ -278,6 +280,60 @@ def bench_attention(torch, dev, iters=10):
     return res
 
 
+def bench_admit(torch, dev, iters=20, with_cpu=True):
+    """Admission for one layer (S=8192 x H=32 token-heads, B=1, D=128): the
+    sensitivity proxy over bf16 K/V, then admit_codes from all-fp16 codes to a
+    budget of half the bytes, and to a tenth with eviction."""
+    import numpy as np
+    from shadowinfer_amd.shadowkv import PrecisionPlan, admit_codes, kv_sensitivity
+
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    gen = torch.Generator(device=dev).manual_seed(77)
+    k, v = make_kv(gen, dev, torch.bfloat16)
+    res = {}
+    kv_sensitivity(k, v)
+    ms = timer.time(lambda: kv_sensitivity(k, v), iters)
+    sens_bytes = 2 * k.numel() * 2 + S * H * 2
+    res["sensitivity_us"] = ms * 1e3
+    res["sensitivity_gbs"] = sens_bytes / (ms * 1e-3) / 1e9
+    sens = kv_sensitivity(k, v).float()
+    imp = torch.rand(S, H, generator=gen, device=dev)
+    codes = torch.ones(S, H, dtype=torch.int8, device=dev)
+    full = S * H * 2 * B * D * 2 * 2
+    for name, budget, evict in (("half", full // 2, False), ("tenth_evict", full // 10, True)):
+        admit_codes(codes, imp, sens, budget, B, D, sink_tokens=4, allow_eviction=evict)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            out, pred, ev = admit_codes(codes, imp, sens, budget, B, D, sink_tokens=4,
+                                        allow_eviction=evict)
+        res[f"admit_{name}_ms"] = (time.perf_counter() - t0) / iters * 1e3
+        res[f"admit_{name}_predicted"] = pred
+        res[f"admit_{name}_evicted"] = ev
+    # sensitivity + admission + plan, as a caller runs them before a pack
+    def plan_step():
+        s_ = kv_sensitivity(k, v).float()
+        out_, _, _ = admit_codes(codes, imp, s_, full // 2, B, D, sink_tokens=4)
+        PrecisionPlan.from_codes(out_)
+    plan_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        plan_step()
+    torch.cuda.synchronize()
+    res["sens_admit_plan_ms"] = (time.perf_counter() - t0) / iters * 1e3
+    if with_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as O
+        c_np, i_np, s_np = codes.cpu().numpy(), imp.cpu().numpy(), sens.cpu().numpy()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            O.admit_codes(c_np, i_np, s_np, full // 2, B, D, 4, True, False)
+        res["cpu_admit_half_ms"] = (time.perf_counter() - t0) / 3 * 1e3
+    return res
+
+
 def cpu_baseline(layers: int = 4):
     """The oracle (C + numpy, one thread) on ``layers`` of the same layers:
     pack + unpack, algorithmic bytes / wall time."""
@@ -329,7 +385,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="same as --part kv")
-    ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "calib"), default="all",
+    ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "admit", "calib"),
+                    default="all",
                     help="run one part only (for profiling); 'calib' runs the plain device "
                          "fill and copy that calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -357,20 +414,22 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "fill + 3 copies", "bytes": CALIB_BYTES}), flush=True)
         return
-    if args.part in ("gemm", "attention"):
-        fn = bench_gemm if args.part == "gemm" else bench_attention
+    if args.part in ("gemm", "attention", "admit"):
+        fn = {"gemm": bench_gemm, "attention": bench_attention, "admit": bench_admit}[args.part]
         log(args.part)
         print(json.dumps({args.part: fn(torch, dev)}), flush=True)
         return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
     log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
-    gemm = attn = None
+    gemm = attn = adm = None
     if args.part == "all":
         log("int8 gemm")
         gemm = bench_gemm(torch, dev)
         log("attention")
         attn = bench_attention(torch, dev)
+        log("admission")
+        adm = bench_admit(torch, dev, with_cpu=not args.no_cpu)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle)")
@@ -419,6 +478,10 @@ def main():
     if attn is not None:
         line["packed_attention"] = {"shape": "B=1, H=32, D=128, S_q=S_kv", "peak_tflops": FP16_PEAK_TFLOPS,
                                     **{s: {k: round(v, 4) for k, v in r.items()} for s, r in attn.items()}}
+    if adm is not None:
+        line["admission"] = {"shape": "S=8192 x H=32 token-heads, B=1, D=128, bf16 K/V",
+                             **{k: (round(v, 4) if isinstance(v, float) else v)
+                                for k, v in adm.items()}}
     print(json.dumps(line), flush=True)
 
 
