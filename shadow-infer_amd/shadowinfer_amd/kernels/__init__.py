@@ -27,6 +27,8 @@ _KERNELS = (
     "int4_kernel",
     "int8_gemm_kernel",
     "fused_attention_kernel",
+    "kv_sensitivity_kernel",
+    "admit_codes_kernel",
 )
 
 
