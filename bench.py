@@ -187,6 +187,28 @@ def bench_kv(torch, dev, steps, warmup):
     torch.cuda.synchronize()
     res["plan_from_codes_ms"] = (time.perf_counter() - t0) / 10 * 1e3
 
+    # Fused compression (working copy + buckets in one pass, 50% of the
+    # entries reused from a previous K/V) on one layer.
+    Lc, Lp = layers[0], layers[1]
+    wk = torch.empty_like(Lc["k"])
+    wv = torch.empty_like(Lc["v"])
+    reuse_u8 = (torch.rand(S * H, generator=gen, device=dev) < 0.5).to(torch.uint8)
+
+    def compress():
+        _native.call("si_kv_pack_copy", Lc["k"].data_ptr(), Lc["v"].data_ptr(), _native.DT_BF16,
+                     B, H, S, D, GROUP, Lc["code"].data_ptr(), Lc["slot"].data_ptr(), Lc["table"],
+                     Lp["k"].data_ptr(), Lp["v"].data_ptr(), reuse_u8.data_ptr(), wk.data_ptr(),
+                     wv.data_ptr(), sptr)
+
+    compress()
+    ms_c = timer.time(compress, 10)
+    n_reuse = int(reuse_u8.sum().item())
+    c_bytes = (dense_in + codes_b + S * H + Lc["packed"] + dense_in
+               + n_reuse * B * D * 2 * 2)  # + previous rows of the reused entries
+    res["compress_us"] = ms_c * 1e3
+    res["compress_gbs"] = c_bytes / (ms_c * 1e-3) / 1e9
+    res["compress_bytes"] = c_bytes
+
     # Reuse (50% mask) and evict (25%) on one layer, for context.
     prev = layers[1]["cache"]
     cur = layers[0]["cache"]

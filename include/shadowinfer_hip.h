@@ -104,6 +104,20 @@ int si_kv_pack(const void* k, const void* v, int dtype, int64_t B, int64_t H, in
                int64_t D, int64_t group, const int8_t* code, const int32_t* slot,
                void* const* buckets, si_stream_t stream);
 
+/* Fused form of ShadowKVAgent._compress_kv_with_plan
+ * (shadowinfer/shadowkv/shadowkv_agent.py:1698-1809) and si_kv_pack: one
+ * pass over K/V writes the buckets (as si_kv_pack) and the dense working
+ * copy out_k/out_v [B, H, S, D] in `dtype`: fp32 entries keep their values,
+ * fp16 entries are rounded to fp16 and back, int8/int4 entries hold their
+ * integer codes (not dequantized), other codes are 0. Entries e with
+ * reuse_mask[e] != 0 (uint8 [S*H], may be NULL) take the rows of
+ * k_prev/v_prev instead (both required when reuse_mask is given). */
+int si_kv_pack_copy(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+                    int64_t D, int64_t group, const int8_t* code, const int32_t* slot,
+                    void* const* buckets, const void* k_prev, const void* v_prev,
+                    const uint8_t* reuse_mask, void* out_k, void* out_v, si_stream_t stream);
+
+
 /* Replaces PackedKVCache.unpack (packed_kv_cache.py:535-577) and
  * _dequantize_int4_bucket (636-656). Writes every element of out_k/out_v
  * ([B, H, S, D] fp32), absent entries as +0.0. scale_dtype: dtype of the

@@ -735,3 +735,51 @@ def admit_budget_greedy(importance, sensitivity, precision_map: Dict[int, Dict[i
                 evicted += 1
             i += 1
     return result, int(predicted), evicted
+
+
+# --------------------------------------------------------------------------
+# Working copy of the plan-driven compression
+# (shadowinfer/shadowkv/shadowkv_agent.py:1698-1809)
+# --------------------------------------------------------------------------
+
+def compress_working_copy(k: np.ndarray, v: np.ndarray, dt: int, codes: np.ndarray,
+                          group_size: int = 16, k_prev: Optional[np.ndarray] = None,
+                          v_prev: Optional[np.ndarray] = None,
+                          reuse_entries: Iterable[Tuple[int, int]] = ()):
+    """The dense ``k``/``v`` of _compress_kv_with_plan: zeros, then per
+    precision group the fp32 values, the fp16 round trip or the int8/int4
+    integer codes cast to the input dtype (index_copy_ of ``qk.to(dtype)``,
+    shadowkv_agent.py:1762-1776), then the reuse entries copied from the
+    previous K/V (:1790-1797). Inputs and outputs in dtype ``dt``."""
+    B, H, S, D = k.shape
+    plan = plan_from_codes(codes)
+    outs = []
+    for x, prev in ((k, k_prev), (v, v_prev)):
+        xf = x.reshape(B, H * S, D)
+        out = np.zeros((B, H * S, D), _np_dtype(dt))
+        for prec in PRECISIONS:
+            flat = plan["flat_indices"][prec]
+            if len(flat) == 0:
+                continue
+            grp = np.ascontiguousarray(xf[:, flat, :].transpose(1, 0, 2))  # [n, B, D]
+            if prec == "fp32":
+                val = grp
+            elif prec == "fp16":
+                val = convert(grp, dt, F16)
+                val = convert(val, F16, dt)
+            else:
+                if prec == "int8":
+                    q, _ = quant_rows_i8(grp, dt)
+                else:
+                    g = group_size if D % group_size == 0 else D
+                    q, _ = quant_rows_i4(grp, dt, g)
+                    q = q.reshape(grp.shape)
+                val = from_f32(q.astype(np.float32), dt)
+            out[:, flat, :] = np.asarray(val).transpose(1, 0, 2)
+        entries = list(reuse_entries)
+        if prev is not None and entries:
+            pf = prev.reshape(B, H * S, D)
+            rflat = np.array([h * S + t for t, h in entries], np.int64)
+            out[:, rflat, :] = pf[:, rflat, :]
+        outs.append(out.reshape(B, H, S, D))
+    return outs[0], outs[1]

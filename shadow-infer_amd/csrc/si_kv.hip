@@ -161,14 +161,47 @@ __device__ __forceinline__ void store_i4(uint8_t* dst, const float* q) {
 }
 
 // ---------------------------------------------------------------------------
+// Dense working copy the pack can write in the same pass: the k/v tensors of
+// ShadowKVAgent._compress_kv_with_plan (shadowinfer/shadowkv/
+// shadowkv_agent.py:1698-1809), [B, H, S, D] in the input dtype. Per entry:
+// fp32 -> the input values, fp16 -> the values rounded to fp16 and back,
+// int8/int4 -> the integer codes (not dequantized), other codes -> 0; entries
+// flagged in `reuse` take the rows of the previous K/V instead.
+// ---------------------------------------------------------------------------
+struct WorkCopy {
+  void* k;
+  void* v;
+  const void* kp;  // previous K/V, read for reuse entries only
+  const void* vp;
+  const uint8_t* reuse;  // [S*H] (token-major) or NULL
+};
+
+// ---------------------------------------------------------------------------
 // Fast pack: D = EPL * LPR, int4 group = EPL * lpg (lpg | LPR, power of two).
 // Grid: blockIdx.y = b*H + h, blockIdx.x = tile of RPP*U tokens; each thread
 // keeps U rows in flight (loads issued before any row is quantized).
 // ---------------------------------------------------------------------------
 
-template <int DT, int LPR>
+// Working-copy values of one chunk -> the 16 bytes of the input dtype.
+template <int DT>
+__device__ __forceinline__ void copy_words(const float* f, uint32_t* w) {
+  if constexpr (DT == SI_DT_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(f[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a = DT == SI_DT_F16 ? f32_to_f16_bits(f[2 * i]) : f32_to_bf16_bits(f[2 * i]);
+      const uint32_t b = DT == SI_DT_F16 ? f32_to_f16_bits(f[2 * i + 1]) : f32_to_bf16_bits(f[2 * i + 1]);
+      w[i] = a | (b << 16);
+    }
+  }
+}
+
+template <int DT, int LPR, bool WC>
 __device__ __forceinline__ void pack_row(const float* xk, const float* xv, int c, int s, int b,
-                                         int B, int lane, int lpg, const Buckets& bk) {
+                                         int B, int lane, int lpg, const Buckets& bk,
+                                         uint32_t* ck, uint32_t* cv) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int D = EPL * LPR;
   const int64_t orow = (int64_t)s * B + b;
@@ -176,11 +209,25 @@ __device__ __forceinline__ void pack_row(const float* xk, const float* xv, int c
   if (c == SI_PREC_FP32) {
     store_f32<EPL>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
     store_f32<EPL>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
+    if constexpr (WC) {
+      copy_words<DT>(xk, ck);
+      copy_words<DT>(xv, cv);
+    }
     return;
   }
   if (c == SI_PREC_FP16) {
     store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
     store_f16<EPL>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+    if constexpr (WC) {
+      float fk[EPL], fv[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        fk[i] = f16_bits_to_f32(f32_to_f16_bits(xk[i]));
+        fv[i] = f16_bits_to_f32(f32_to_f16_bits(xv[i]));
+      }
+      copy_words<DT>(fk, ck);
+      copy_words<DT>(fv, cv);
+    }
     return;
   }
   // int8 (per row) or int4 (per group): shared arithmetic.
@@ -216,6 +263,16 @@ __device__ __forceinline__ void pack_row(const float* xk, const float* xv, int c
   for (int i = 0; i < EPL; ++i) {
     qk[i] = clampf(quant_quotient<DT>(xk[i], sk, rk, fk), lo, hi);
     qv[i] = clampf(quant_quotient<DT>(xv[i], sv, rv, fv), lo, hi);
+  }
+  if constexpr (WC) {
+    float fk2[EPL], fv2[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      fk2[i] = qk[i] + 0.0f;  // the integer code as a value (-0 -> +0)
+      fv2[i] = qv[i] + 0.0f;
+    }
+    copy_words<DT>(fk2, ck);
+    copy_words<DT>(fv2, cv);
   }
   if (i8) {
     store_i8<EPL>(reinterpret_cast<int8_t*>(bk.p[8]) + oel, qk);
@@ -330,10 +387,17 @@ __device__ __forceinline__ uint32_t bytes4(uint32_t a, uint32_t b, uint32_t c, u
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-template <int LPR>
+// Two integer codes (words from quant_bf16) -> their bf16 values in one word.
+__device__ __forceinline__ uint32_t codes_bf16x2(uint32_t q0, uint32_t q1) {
+  const uint32_t a = __float_as_uint(__uint_as_float(q0) - kMagic) >> 16;  // exact in bf16
+  const uint32_t b = __float_as_uint(__uint_as_float(q1) - kMagic) & 0xffff0000u;
+  return a | b;
+}
+
+template <int LPR, bool WC>
 __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32_t wv[4], int c,
                                               int s, int b, int B, int lane, int lpg,
-                                              const Buckets& bk) {
+                                              const Buckets& bk, uint32_t* ck, uint32_t* cv) {
   constexpr int D = 8 * LPR;
   const int64_t orow = (int64_t)s * B + b;
   const int64_t oel = orow * D + lane * 8;
@@ -349,9 +413,26 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
     if (c == SI_PREC_FP16) {
       store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
       store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+      if constexpr (WC) {
+        float fk[8], fv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          fk[i] = f16_bits_to_f32(f32_to_f16_bits(xk[i]));
+          fv[i] = f16_bits_to_f32(f32_to_f16_bits(xv[i]));
+        }
+        copy_words<SI_DT_BF16>(fk, ck);
+        copy_words<SI_DT_BF16>(fv, cv);
+      }
     } else {
       store_f32<8>(reinterpret_cast<float*>(bk.p[0]) + oel, xk);
       store_f32<8>(reinterpret_cast<float*>(bk.p[1]) + oel, xv);
+      if constexpr (WC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ck[i] = wk[i];
+          cv[i] = wv[i];
+        }
+      }
     }
     return;
   }
@@ -376,6 +457,13 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
     qk[2 * i + 1] = quant_bf16(__uint_as_float(wk[i] & 0xffff0000u), sk, rk, fk, lo, hi);
     qv[2 * i] = quant_bf16(__uint_as_float(wv[i] << 16), sv, rv, fv, lo, hi);
     qv[2 * i + 1] = quant_bf16(__uint_as_float(wv[i] & 0xffff0000u), sv, rv, fv, lo, hi);
+  }
+  if constexpr (WC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ck[i] = codes_bf16x2(qk[2 * i], qk[2 * i + 1]);
+      cv[i] = codes_bf16x2(qv[2 * i], qv[2 * i + 1]);
+    }
   }
   if (i8) {
     *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(bk.p[8]) + oel) =
@@ -409,12 +497,35 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
   }
 }
 
-template <int DT, int LPR, int U>
+// 16 bytes of the working copy at byte offset `off`: the computed chunk, or
+// the previous K/V when the entry is reused.
+template <bool WC>
+__device__ __forceinline__ void store_copy(const WorkCopy& wc, int64_t off, bool reuse,
+                                           uint32_t* ck, uint32_t* cv) {
+  if constexpr (WC) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    if (reuse) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(wc.kp) + off);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(wc.vp) + off);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ck[i] = a[i];
+        cv[i] = b[i];
+      }
+    }
+    __builtin_nontemporal_store(u32x4{ck[0], ck[1], ck[2], ck[3]},
+                                reinterpret_cast<u32x4*>(reinterpret_cast<char*>(wc.k) + off));
+    __builtin_nontemporal_store(u32x4{cv[0], cv[1], cv[2], cv[3]},
+                                reinterpret_cast<u32x4*>(reinterpret_cast<char*>(wc.v) + off));
+  }
+}
+
+template <int DT, int LPR, int U, bool WC>
 __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin,
                                                     const void* __restrict__ vin, int B, int H,
                                                     int S, int lpg, const int8_t* __restrict__ code,
                                                     const int32_t* __restrict__ slot,
-                                                    Buckets bk) {
+                                                    Buckets bk, WorkCopy wc) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int D = EPL * LPR;
   constexpr int RPP = 256 / LPR;  // rows per pass of the block
@@ -426,6 +537,7 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
   const int t0 = blockIdx.x * (RPP * U) + sub;
   const int64_t row0 = (int64_t)bh * S;
   int c[U], s[U];
+  bool ru[U];  // reused entry (working copy only)
   if constexpr (DT == SI_DT_BF16) {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     uint32_t wk[U][4], wv[U][4];
@@ -434,6 +546,7 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
       const int t = t0 + u * RPP;
       c[u] = SI_PREC_EVICTED;
       s[u] = 0;
+      ru[u] = false;
       if (t < S) {
         const int e = t * H + h;
         const int64_t off = ((row0 + t) * D + lane * EPL) * 2;
@@ -448,11 +561,16 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
         }
         c[u] = code[e];
         s[u] = slot[e];
+        ru[u] = WC && wc.reuse != nullptr && wc.reuse[e] != 0;
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c[u] >= 0 && c[u] <= 3) pack_row_bf16<LPR>(wk[u], wv[u], c[u], s[u], b, B, lane, lpg, bk);
+      uint32_t ck[4] = {0u, 0u, 0u, 0u}, cv[4] = {0u, 0u, 0u, 0u};
+      if (c[u] >= 0 && c[u] <= 3)
+        pack_row_bf16<LPR, WC>(wk[u], wv[u], c[u], s[u], b, B, lane, lpg, bk, ck, cv);
+      if (WC && t0 + u * RPP < S)
+        store_copy<WC>(wc, ((row0 + t0 + u * RPP) * D + lane * EPL) * 2, ru[u], ck, cv);
     }
   } else {
     float xk[U][EPL], xv[U][EPL];
@@ -461,17 +579,24 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
       const int t = t0 + u * RPP;
       c[u] = SI_PREC_EVICTED;
       s[u] = 0;
+      ru[u] = false;
       if (t < S) {
         const int e = t * H + h;
         load_chunk<DT>(kin, (row0 + t) * D + lane * EPL, xk[u]);
         load_chunk<DT>(vin, (row0 + t) * D + lane * EPL, xv[u]);
         c[u] = code[e];
         s[u] = slot[e];
+        ru[u] = WC && wc.reuse != nullptr && wc.reuse[e] != 0;
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c[u] >= 0 && c[u] <= 3) pack_row<DT, LPR>(xk[u], xv[u], c[u], s[u], b, B, lane, lpg, bk);
+      uint32_t ck[4] = {0u, 0u, 0u, 0u}, cv[4] = {0u, 0u, 0u, 0u};
+      if (c[u] >= 0 && c[u] <= 3)
+        pack_row<DT, LPR, WC>(xk[u], xv[u], c[u], s[u], b, B, lane, lpg, bk, ck, cv);
+      if (WC && t0 + u * RPP < S)
+        store_copy<WC>(wc, ((row0 + t0 + u * RPP) * D + lane * EPL) * (DT == SI_DT_F32 ? 4 : 2),
+                       ru[u], ck, cv);
     }
   }
 }
@@ -483,7 +608,7 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
 template <int DT>
 __device__ void pack_entry_generic(const void* in, int64_t B, int64_t H, int64_t S, int64_t D,
                                    int64_t g, int64_t t, int64_t h, int c, int64_t s,
-                                   void* data, void* scale) {
+                                   void* data, void* scale, void* copy) {
   const int64_t L = B * D;
   const int64_t rb = (L + 1) / 2;
   const int64_t G = D / g;
@@ -492,9 +617,12 @@ __device__ void pack_entry_generic(const void* in, int64_t B, int64_t H, int64_t
     const int64_t src = ((b * H + h) * S + t) * D;
     const int64_t orow = s * B + b;
     if (c == SI_PREC_FP32 || c == SI_PREC_FP16) {
-      for (int64_t d = 0; d < D; ++d)
-        store_any(data, c == SI_PREC_FP32 ? SI_DT_F32 : SI_DT_F16, orow * D + d,
-                  load_any(in, DT, src + d));
+      for (int64_t d = 0; d < D; ++d) {
+        const float x = load_any(in, DT, src + d);
+        store_any(data, c == SI_PREC_FP32 ? SI_DT_F32 : SI_DT_F16, orow * D + d, x);
+        if (copy != nullptr)
+          store_any(copy, DT, src + d, c == SI_PREC_FP32 ? x : f16_bits_to_f32(f32_to_f16_bits(x)));
+      }
       continue;
     }
     const bool i8 = (c == SI_PREC_INT8);
@@ -508,6 +636,7 @@ __device__ void pack_entry_generic(const void* in, int64_t B, int64_t H, int64_t
         const float x = load_any(in, DT, src + g0 + d);
         const float q = clampf(quant_quotient<DT>(x, sc, 0.0f, false), i8 ? -128.0f : -8.0f,
                                i8 ? 127.0f : 7.0f);
+        if (copy != nullptr) store_any(copy, DT, src + g0 + d, q + 0.0f);
         if (i8) {
           reinterpret_cast<int8_t*>(data)[orow * D + g0 + d] = (int8_t)(int)q;
         } else {
@@ -532,17 +661,32 @@ __global__ __launch_bounds__(256) void kv_pack_generic(const void* __restrict__ 
                                                        int64_t H, int64_t S, int64_t D,
                                                        int64_t g, const int8_t* __restrict__ code,
                                                        const int32_t* __restrict__ slot,
-                                                       Buckets bk) {
+                                                       Buckets bk, WorkCopy wc) {
   const int64_t n = S * H;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int c = code[e];
-    if (c < 0 || c > 3) continue;
     const int64_t t = e / H;
     const int64_t h = e - t * H;
-    const int64_t s = slot[e];
-    pack_entry_generic<DT>(kin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 0], bk.p[4 * c + 2]);
-    pack_entry_generic<DT>(vin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 1], bk.p[4 * c + 3]);
+    const bool packed = c >= 0 && c <= 3;
+    if (packed) {
+      const int64_t s = slot[e];
+      pack_entry_generic<DT>(kin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 0], bk.p[4 * c + 2],
+                             wc.k);
+      pack_entry_generic<DT>(vin, B, H, S, D, g, t, h, c, s, bk.p[4 * c + 1], bk.p[4 * c + 3],
+                             wc.v);
+    }
+    if (wc.k == nullptr) continue;
+    const bool reuse = wc.reuse != nullptr && wc.reuse[e] != 0;
+    if (!reuse && packed) continue;
+    // Working copy of a reused (previous K/V) or unpacked (zero) entry.
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t src = ((b * H + h) * S + t) * D;
+      for (int64_t d = 0; d < D; ++d) {
+        store_any(wc.k, DT, src + d, reuse ? load_any(wc.kp, DT, src + d) : 0.0f);
+        store_any(wc.v, DT, src + d, reuse ? load_any(wc.vp, DT, src + d) : 0.0f);
+      }
+    }
   }
 }
 
@@ -800,12 +944,16 @@ bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 template <int DT>
 int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, int64_t D,
                 int64_t g, const int8_t* code, const int32_t* slot, const Buckets& bk,
-                hipStream_t st) {
+                const WorkCopy& wc, hipStream_t st) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int U = 2;
   const int64_t lpr = D / EPL;
   const int64_t lpg = g / EPL;
-  const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                         reinterpret_cast<uintptr_t>(wc.k) | reinterpret_cast<uintptr_t>(wc.v) |
+                         reinterpret_cast<uintptr_t>(wc.kp) | reinterpret_cast<uintptr_t>(wc.vp)) &
+                        15) == 0;
+  const bool copy = wc.k != nullptr;
   const bool small = B * H < 65536 && S * H < ((int64_t)1 << 31) && B * H * S * D < ((int64_t)1 << 40);
   const bool fast = aligned && small && D % EPL == 0 && pow2(lpr) && lpr >= 4 && lpr <= 64 &&
                     g % EPL == 0 && pow2(lpg) && lpg <= lpr;
@@ -814,8 +962,12 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
     const dim3 grid((unsigned)ceil_div(S, rpb), (unsigned)(B * H));
 #define SI_PACK_CASE(L)                                                                     \
   case L:                                                                                   \
-    kv_pack_fast<DT, L, U><<<grid, 256, 0, st>>>(k, v, (int)B, (int)H, (int)S, (int)lpg,    \
-                                                 code, slot, bk);                           \
+    if (copy)                                                                               \
+      kv_pack_fast<DT, L, U, true><<<grid, 256, 0, st>>>(k, v, (int)B, (int)H, (int)S,      \
+                                                         (int)lpg, code, slot, bk, wc);     \
+    else                                                                                    \
+      kv_pack_fast<DT, L, U, false><<<grid, 256, 0, st>>>(k, v, (int)B, (int)H, (int)S,     \
+                                                          (int)lpg, code, slot, bk, wc);    \
     break;
     switch (lpr) {
       SI_PACK_CASE(4)
@@ -827,7 +979,8 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
 #undef SI_PACK_CASE
     return check_launch("si_kv_pack/fast");
   }
-  kv_pack_generic<DT><<<grid_for(S * H, 256), 256, 0, st>>>(k, v, B, H, S, D, g, code, slot, bk);
+  kv_pack_generic<DT><<<grid_for(S * H, 256), 256, 0, st>>>(k, v, B, H, S, D, g, code, slot, bk,
+                                                              wc);
   return check_launch("si_kv_pack/generic");
 }
 
@@ -871,10 +1024,37 @@ extern "C" int si_kv_pack(const void* k, const void* v, int dtype, int64_t B, in
   SI_CHECK_ARG(k && v && code && slot, "si_kv_pack: NULL input");
   const Buckets bk = to_buckets(buckets);
   hipStream_t st = as_stream(stream);
+  const WorkCopy none{nullptr, nullptr, nullptr, nullptr, nullptr};
   switch (dtype) {
-    case SI_DT_F32: return launch_pack<SI_DT_F32>(k, v, B, H, S, D, group, code, slot, bk, st);
-    case SI_DT_F16: return launch_pack<SI_DT_F16>(k, v, B, H, S, D, group, code, slot, bk, st);
-    default: return launch_pack<SI_DT_BF16>(k, v, B, H, S, D, group, code, slot, bk, st);
+    case SI_DT_F32: return launch_pack<SI_DT_F32>(k, v, B, H, S, D, group, code, slot, bk, none, st);
+    case SI_DT_F16: return launch_pack<SI_DT_F16>(k, v, B, H, S, D, group, code, slot, bk, none, st);
+    default: return launch_pack<SI_DT_BF16>(k, v, B, H, S, D, group, code, slot, bk, none, st);
+  }
+}
+
+extern "C" int si_kv_pack_copy(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                               int64_t S, int64_t D, int64_t group, const int8_t* code,
+                               const int32_t* slot, void* const* buckets, const void* k_prev,
+                               const void* v_prev, const uint8_t* reuse_mask, void* out_k,
+                               void* out_v, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_kv_pack_copy: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0, "si_kv_pack_copy: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_pack_copy: group %lld must divide D %lld",
+               (long long)group, (long long)D);
+  SI_CHECK_ARG(buckets != nullptr, "si_kv_pack_copy: buckets table is NULL");
+  if (B * H * S == 0) return SI_OK;
+  SI_CHECK_ARG(k && v && code && slot && out_k && out_v, "si_kv_pack_copy: NULL input or output");
+  SI_CHECK_ARG(reuse_mask == nullptr || (k_prev != nullptr && v_prev != nullptr),
+               "si_kv_pack_copy: reuse_mask needs k_prev and v_prev");
+  const Buckets bk = to_buckets(buckets);
+  hipStream_t st = as_stream(stream);
+  const WorkCopy wc{out_k, out_v, reuse_mask ? k_prev : nullptr, reuse_mask ? v_prev : nullptr,
+                    reuse_mask};
+  switch (dtype) {
+    case SI_DT_F32: return launch_pack<SI_DT_F32>(k, v, B, H, S, D, group, code, slot, bk, wc, st);
+    case SI_DT_F16: return launch_pack<SI_DT_F16>(k, v, B, H, S, D, group, code, slot, bk, wc, st);
+    default: return launch_pack<SI_DT_BF16>(k, v, B, H, S, D, group, code, slot, bk, wc, st);
   }
 }
 

@@ -2,6 +2,7 @@
 rate-distortion admission that chooses the precisions, and the fused
 packed-KV attention."""
 
+from .compress import compress_kv_with_plan
 from .packed_attention import packed_attention
 from .packed_kv_cache import PackedKVCache
 from .rd_allocator import (
@@ -31,6 +32,7 @@ __all__ = [
     "admit_budget",
     "admit_codes",
     "codes_to_map",
+    "compress_kv_with_plan",
     "entry_bytes",
     "kv_sensitivity",
     "map_to_codes",

@@ -67,7 +67,11 @@ class PackedKVCache:
 
     def _do_pack(self, k_tensor: torch.Tensor, v_tensor: torch.Tensor,
                  precision_map: Optional[Dict[int, Dict[int, str]]], group_size: int = 16,
-                 plan: Any = None, precomputed: Optional[Dict[str, Any]] = None) -> None:
+                 plan: Any = None, precomputed: Optional[Dict[str, Any]] = None,
+                 work_copy: Optional[Tuple[Any, ...]] = None) -> None:
+        """``work_copy`` = (out_k, out_v, k_prev, v_prev, reuse_u8) makes the same
+        pass write the dense working copy of the plan-driven compression
+        (``si_kv_pack_copy``)."""
         B, H, S, D = k_tensor.shape
         if plan is not None:
             # packed_kv_cache.py:238-251
@@ -109,9 +113,16 @@ class PackedKVCache:
         self._scale_dtype = k.dtype
         self._buckets = self._alloc_buckets(grouping.counts, dev, k.dtype)
         self._view = None
-        _native.call("si_kv_pack", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,
-                     grouping.code.data_ptr(), grouping.slot.data_ptr(), self._bucket_table(),
-                     _native.stream(dev))
+        if work_copy is None:
+            _native.call("si_kv_pack", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,
+                         grouping.code.data_ptr(), grouping.slot.data_ptr(), self._bucket_table(),
+                         _native.stream(dev))
+        else:
+            out_k, out_v, k_prev, v_prev, reuse = work_copy
+            _native.call("si_kv_pack_copy", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,
+                         grouping.code.data_ptr(), grouping.slot.data_ptr(), self._bucket_table(),
+                         _native.ptr(k_prev), _native.ptr(v_prev), _native.ptr(reuse),
+                         out_k.data_ptr(), out_v.data_ptr(), _native.stream(dev))
         if precomputed:
             self._apply_precomputed(precomputed, grouping.counts)
 
