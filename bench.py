@@ -14,11 +14,12 @@ Also reported on the same JSON line: per-kernel times with the roofline of the
 dominant kernel, the INT8 FFN GEMM (4096 x 11008, M in {16, 64, 256, 1024}) in
 TOPS against the int8 MFMA peak, the fused packed-KV attention, the
 rate-distortion admission of one layer (sensitivity proxy + budget solver),
+the paged KV store of one layer (prefill append, append, gather),
 and the CPU baseline (the oracle on the host, a bounded sample of the same
 workload).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--part all|kv|gemm|attention|admit|calib]
+                       [--part all|kv|gemm|attention|admit|paged|calib]
 """
 
 from __future__ import annotations
@@ -356,6 +357,42 @@ def bench_admit(torch, dev, iters=20, with_cpu=True):
     return res
 
 
+def bench_paged(torch, dev, iters=10):
+    """PagedKVStore for one layer (B=1, H=32, D=128, bf16): an 8192-token
+    int8 prefill into 32-token pages, a 64-token append, and gather (every
+    page decoded to fp32 [1, 32, 8192, 128] in one launch)."""
+    from shadowinfer_amd.shadowkv import PagedKVStore
+
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    gen = torch.Generator(device=dev).manual_seed(91)
+    k, v = make_kv(gen, dev, torch.bfloat16)
+    res = {}
+    st = PagedKVStore(B, H, D, page_size=32, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    st.append(k, v, "int8")
+    torch.cuda.synchronize()
+    res["prefill_append_ms"] = (time.perf_counter() - t0) * 1e3
+    res["pages"] = st.page_count
+    st.gather()
+    ms = timer.time(st.gather, iters)
+    payload = st.data_plane_bytes()
+    out_bytes = 2 * B * H * S * D * 4
+    res["gather_us"] = ms * 1e3
+    res["gather_bytes"] = payload + out_bytes
+    res["gather_gbs"] = (payload + out_bytes) / (ms * 1e-3) / 1e9
+    st2 = PagedKVStore(B, H, D, page_size=32, device=dev)
+    st2.append(k[:, :, :8128], v[:, :, :8128], "int8")
+    kn, vn = k[:, :, 8128:].contiguous(), v[:, :, 8128:].contiguous()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    st2.append(kn, vn, "int8")
+    torch.cuda.synchronize()
+    res["append_64_tokens_us"] = (time.perf_counter() - t0) * 1e6
+    return res
+
+
 def cpu_baseline(layers: int = 4):
     """The oracle (C + numpy, one thread) on ``layers`` of the same layers:
     pack + unpack, algorithmic bytes / wall time."""
@@ -407,7 +444,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="same as --part kv")
-    ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "admit", "calib"),
+    ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "admit", "paged",
+                                       "calib"),
                     default="all",
                     help="run one part only (for profiling); 'calib' runs the plain device "
                          "fill and copy that calibrate the HBM byte counters")
@@ -436,15 +474,16 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "fill + 3 copies", "bytes": CALIB_BYTES}), flush=True)
         return
-    if args.part in ("gemm", "attention", "admit"):
-        fn = {"gemm": bench_gemm, "attention": bench_attention, "admit": bench_admit}[args.part]
+    if args.part in ("gemm", "attention", "admit", "paged"):
+        fn = {"gemm": bench_gemm, "attention": bench_attention, "admit": bench_admit,
+              "paged": bench_paged}[args.part]
         log(args.part)
         print(json.dumps({args.part: fn(torch, dev)}), flush=True)
         return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
     log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
-    gemm = attn = adm = None
+    gemm = attn = adm = paged = None
     if args.part == "all":
         log("int8 gemm")
         gemm = bench_gemm(torch, dev)
@@ -452,6 +491,8 @@ def main():
         attn = bench_attention(torch, dev)
         log("admission")
         adm = bench_admit(torch, dev, with_cpu=not args.no_cpu)
+        log("paged store")
+        paged = bench_paged(torch, dev)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle)")
@@ -500,6 +541,10 @@ def main():
     if attn is not None:
         line["packed_attention"] = {"shape": "B=1, H=32, D=128, S_q=S_kv", "peak_tflops": FP16_PEAK_TFLOPS,
                                     **{s: {k: round(v, 4) for k, v in r.items()} for s, r in attn.items()}}
+    if paged is not None:
+        line["paged_kv_store"] = {"shape": "B=1, H=32, D=128, bf16 K/V, int8 pages of 32 tokens",
+                                  **{k: (round(v, 4) if isinstance(v, float) else v)
+                                     for k, v in paged.items()}}
     if adm is not None:
         line["admission"] = {"shape": "S=8192 x H=32 token-heads, B=1, D=128, bf16 K/V",
                              **{k: (round(v, 4) if isinstance(v, float) else v)

@@ -241,6 +241,34 @@ int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64
                            si_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
+/* Paged KV store                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces the row quantization and page write of PagedKVStore.append and
+ * rewrite_tokens (shadowinfer/shadowkv/paged_kv_store.py:189-212, 248-307,
+ * 407-447): tokens t0 .. t0+take-1 of k, v [B, H, T, D] (`dtype`) go to rows
+ * offset .. offset+take-1 of a page of `capacity` rows per (b, h).
+ * page: HOST array of 4 device pointers {k, v, scale_k, scale_v}:
+ *   precision 0 ("fp32" page): k, v [B, H, capacity, D] in `dtype` (a copy)
+ *   precision 1: k, v [B, H, capacity, D] fp16
+ *   precision 2: k, v int8 [B, H, capacity, D]; scales [B, H, capacity, 1] in `dtype`
+ *   precision 3: k, v uint8 [B, H, capacity, ceil(D/2)] (code + 8, high
+ *                nibble first); scales [B, H, capacity, D/group, 1] in `dtype`
+ * The row arithmetic is si_kv_pack's, so page rows equal packed-cache rows. */
+int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t T,
+                  int64_t D, int64_t t0, int64_t take, int precision, int64_t group,
+                  void* const* page, int64_t capacity, int64_t offset, si_stream_t stream);
+
+/* Replaces PagedKVStore.gather / _decode (paged_kv_store.py:326-405): every
+ * page of the device table (int64 [n_pages, 8] rows {precision, k, v,
+ * scale_k, scale_v, start token, tokens, capacity}) decoded into fp32
+ * out_k/out_v [B, H, S, D] at its start token; rows no page covers are left
+ * as they are (the caller zeroes them). `dtype`: the input dtype of the pages. */
+int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, int64_t B, int64_t H,
+                   int64_t S, int64_t D, int64_t group, float* out_k, float* out_v,
+                   si_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
 /* Rate-distortion admission                                               */
 /* ---------------------------------------------------------------------- */
 

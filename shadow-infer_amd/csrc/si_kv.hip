@@ -929,6 +929,197 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Paged store (PagedKVStore, shadowinfer/shadowkv/paged_kv_store.py). A page
+// holds one precision for tokens [start, start + n) of every (b, h) in
+// capacity buffers [B, H, P, ...]: payload rows of D values in the input
+// dtype ("fp32" pages keep the input as it is, :189-193), fp16, int8, or
+// ceil(D/2) int4 bytes (high nibble first, code + 8), with per-row int8
+// scales [B, H, P, 1] and per-group int4 scales [B, H, P, G, 1] in the input
+// dtype. Quantization is the pack's row arithmetic, so page rows equal the
+// rows PackedKVCache would hold.
+// ---------------------------------------------------------------------------
+
+// Writes tokens t0 .. t0+take-1 of k/v [B, H, T, D] into rows off .. of the
+// page (append :248-307, rewrite_tokens :407-447). Page pointers sit in the
+// bucket slots of `prec`. Grid: blockIdx.y = b*H + h.
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void page_write_fast(const void* __restrict__ kin,
+                                                       const void* __restrict__ vin, int T, int t0,
+                                                       int take, int P, int off, int prec, int lpg,
+                                                       Buckets pg) {
+  constexpr int EPL = Chunk<DT>::EPL;
+  constexpr int D = EPL * LPR;
+  constexpr int RPP = 256 / LPR;
+  constexpr int ES = DT == SI_DT_F32 ? 4 : 2;
+  const int lane = threadIdx.x % LPR;
+  const int j = blockIdx.x * RPP + threadIdx.x / LPR;
+  if (j >= take) return;
+  const int64_t bh = blockIdx.y;
+  const int64_t src = (bh * T + t0 + j) * D + lane * EPL;
+  const int dst = (int)(bh * P + off + j);
+  if (prec == SI_PREC_FP32) {  // the input dtype, unchanged
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + src * ES);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vin) + src * ES);
+    const int64_t o = ((int64_t)dst * D + lane * EPL) * ES;
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(pg.p[0]) + o) = a;
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(pg.p[1]) + o) = b;
+    return;
+  }
+  float xk[EPL], xv[EPL];
+  load_chunk<DT>(kin, src, xk);
+  load_chunk<DT>(vin, src, xv);
+  pack_row<DT, LPR, false>(xk, xv, prec, dst, 0, 1, lane, lpg, pg, nullptr, nullptr);
+}
+
+// Any D and group: one thread per (b, h, token) row.
+template <int DT>
+__global__ __launch_bounds__(256) void page_write_generic(const void* __restrict__ kin,
+                                                          const void* __restrict__ vin, int64_t BH,
+                                                          int64_t T, int64_t D, int64_t t0,
+                                                          int64_t take, int64_t P, int64_t off,
+                                                          int prec, int64_t g, Buckets pg) {
+  constexpr int ES = DT == SI_DT_F32 ? 4 : 2;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < BH * take;
+       r += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t bh = r / take;
+    const int64_t j = r - bh * take;
+    const int64_t src = (bh * T + t0 + j) * D;
+    const int64_t dst = bh * P + off + j;
+    if (prec == SI_PREC_FP32) {
+      for (int64_t d = 0; d < D * ES; ++d) {
+        reinterpret_cast<char*>(pg.p[0])[dst * D * ES + d] = reinterpret_cast<const char*>(kin)[src * ES + d];
+        reinterpret_cast<char*>(pg.p[1])[dst * D * ES + d] = reinterpret_cast<const char*>(vin)[src * ES + d];
+      }
+      continue;
+    }
+    const char* kr = reinterpret_cast<const char*>(kin) + src * ES;
+    const char* vr = reinterpret_cast<const char*>(vin) + src * ES;
+    pack_entry_generic<DT>(kr, 1, 1, 1, D, g, 0, 0, prec, dst, pg.p[4 * prec + 0],
+                           pg.p[4 * prec + 2], nullptr);
+    pack_entry_generic<DT>(vr, 1, 1, 1, D, g, 0, 0, prec, dst, pg.p[4 * prec + 1],
+                           pg.p[4 * prec + 3], nullptr);
+  }
+}
+
+// One page-table row: precision, k, v, scale_k, scale_v, start token, tokens,
+// capacity (int64 each).
+struct PageRow {
+  int64_t prec, k, v, sk, sv, start, ntok, cap;
+};
+
+template <int SDT>
+__device__ __forceinline__ float page_value(const PageRow& pr, int j, int64_t row, int64_t d,
+                                            int64_t D, int64_t g) {
+  const int64_t e = row * D + d;
+  switch (pr.prec) {
+    case SI_PREC_FP32: return load_any(reinterpret_cast<const void*>(j ? pr.v : pr.k), SDT, e);
+    case SI_PREC_FP16:
+      return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(j ? pr.v : pr.k)[e]);
+    case SI_PREC_INT8:
+      return (float)reinterpret_cast<const int8_t*>(j ? pr.v : pr.k)[e] *
+             load_any(reinterpret_cast<const void*>(j ? pr.sv : pr.sk), SDT, row);
+    default: {
+      const int64_t rb = (D + 1) / 2;
+      const uint32_t byte = reinterpret_cast<const uint8_t*>(j ? pr.v : pr.k)[row * rb + d / 2];
+      const int nib = (d & 1) ? (int)(byte & 0xfu) : (int)(byte >> 4);
+      return (float)(nib - 8) *
+             load_any(reinterpret_cast<const void*>(j ? pr.sv : pr.sk), SDT, row * (D / g) + d / g);
+    }
+  }
+}
+
+// Four consecutive values (one group) of a page row, decoded to fp32.
+template <int SDT, int PREC>
+__device__ __forceinline__ void page_values4(const void* pay, const void* sc, int64_t row,
+                                             int d, int D, int g, float* o) {
+  if constexpr (PREC == SI_PREC_FP32) {  // the input dtype
+    if constexpr (SDT == SI_DT_F32) {
+      const float4 x = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(pay) + row * D + d);
+      o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(pay) + row * D + d);
+      const uint32_t w[2] = {x.x, x.y};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        o[2 * i] = SDT == SI_DT_BF16 ? bf16_bits_to_f32(w[i] & 0xffffu) : f16_bits_to_f32(w[i] & 0xffffu);
+        o[2 * i + 1] = SDT == SI_DT_BF16 ? bf16_bits_to_f32(w[i] >> 16) : f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  } else if constexpr (PREC == SI_PREC_FP16) {
+    const uint2 x = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(pay) + row * D + d);
+    o[0] = f16_bits_to_f32(x.x & 0xffffu);
+    o[1] = f16_bits_to_f32(x.x >> 16);
+    o[2] = f16_bits_to_f32(x.y & 0xffffu);
+    o[3] = f16_bits_to_f32(x.y >> 16);
+  } else if constexpr (PREC == SI_PREC_INT8) {
+    const uint32_t x = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(pay) + row * D + d);
+    const float s = load_any(sc, SDT, row);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (float)(int8_t)(x >> (8 * i)) * s;
+  } else {
+    const uint32_t x = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(pay) + row * (D / 2) + d / 2);
+    const float s = load_any(sc, SDT, row * (D / g) + d / g);
+    o[0] = (float)((int)((x >> 4) & 0xfu) - 8) * s;
+    o[1] = (float)((int)(x & 0xfu) - 8) * s;
+    o[2] = (float)((int)((x >> 12) & 0xfu) - 8) * s;
+    o[3] = (float)((int)((x >> 8) & 0xfu) - 8) * s;
+  }
+}
+
+template <int SDT, int PREC>
+__device__ __forceinline__ void gather_page_vec(const PageRow& pr, int64_t bh, int64_t S, int D,
+                                                int g, float* __restrict__ ok,
+                                                float* __restrict__ ov) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int n4 = (int)pr.ntok * (D / 4);
+  const int q4 = D / 4;
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+    const int jt = i / q4;
+    const int d = (i - jt * q4) * 4;
+    const int64_t row = bh * pr.cap + jt;
+    const int64_t o = (bh * S + pr.start + jt) * D + d;
+    float a[4], b[4];
+    page_values4<SDT, PREC>(reinterpret_cast<const void*>(pr.k), reinterpret_cast<const void*>(pr.sk), row, d, D, g, a);
+    page_values4<SDT, PREC>(reinterpret_cast<const void*>(pr.v), reinterpret_cast<const void*>(pr.sv), row, d, D, g, b);
+    __builtin_nontemporal_store(f32x4{a[0], a[1], a[2], a[3]}, reinterpret_cast<f32x4*>(ok + o));
+    __builtin_nontemporal_store(f32x4{b[0], b[1], b[2], b[3]}, reinterpret_cast<f32x4*>(ov + o));
+  }
+}
+
+// gather (:326-405): every page's rows decoded to fp32 [B, H, S, D] in one
+// launch. Grid: blockIdx.x = page, blockIdx.y = b*H + h. VEC: four values of
+// one group per thread, loads and 16-byte stores specialised for the page's
+// precision (D % 4 == 0, group % 4 == 0, 16-byte aligned rows).
+template <int SDT, bool VEC>
+__global__ __launch_bounds__(256) void page_gather_kernel(const int64_t* __restrict__ table,
+                                                          int64_t S, int64_t D, int64_t g,
+                                                          float* __restrict__ ok,
+                                                          float* __restrict__ ov) {
+  const int64_t* t = table + (int64_t)blockIdx.x * 8;
+  const PageRow pr{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+  const int64_t bh = blockIdx.y;
+  if constexpr (VEC) {
+    switch ((int)pr.prec) {
+      case SI_PREC_FP32: gather_page_vec<SDT, SI_PREC_FP32>(pr, bh, S, (int)D, (int)g, ok, ov); break;
+      case SI_PREC_FP16: gather_page_vec<SDT, SI_PREC_FP16>(pr, bh, S, (int)D, (int)g, ok, ov); break;
+      case SI_PREC_INT8: gather_page_vec<SDT, SI_PREC_INT8>(pr, bh, S, (int)D, (int)g, ok, ov); break;
+      default: gather_page_vec<SDT, SI_PREC_INT4>(pr, bh, S, (int)D, (int)g, ok, ov); break;
+    }
+  } else {
+    const int64_t n = pr.ntok * D;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const int64_t jt = i / D;
+      const int64_t d = i - jt * D;
+      const int64_t row = bh * pr.cap + jt;
+      const int64_t o = (bh * S + pr.start + jt) * D + d;
+      ok[o] = page_value<SDT>(pr, 0, row, d, D, g);
+      ov[o] = page_value<SDT>(pr, 1, row, d, D, g);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -1138,4 +1329,96 @@ extern "C" int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
       old_code, old_slot, to_buckets(old_buckets), new_code, new_slot, to_buckets(new_buckets), n,
       geo);
   return check_launch("si_kv_compact");
+}
+
+extern "C" int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                             int64_t T, int64_t D, int64_t t0, int64_t take, int precision,
+                             int64_t group, void* const* page, int64_t capacity, int64_t offset,
+                             si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_page_write: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(precision >= SI_PREC_FP32 && precision <= SI_PREC_INT4,
+               "si_page_write: precision %d is not 0..3", precision);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && T >= 0 && D > 0 && take >= 0 && t0 >= 0 && t0 + take <= T,
+               "si_page_write: tokens [%lld, %lld) outside [0, %lld)", (long long)t0,
+               (long long)(t0 + take), (long long)T);
+  SI_CHECK_ARG(offset >= 0 && offset + take <= capacity,
+               "si_page_write: rows [%lld, %lld) outside the page capacity %lld",
+               (long long)offset, (long long)(offset + take), (long long)capacity);
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_page_write: group must divide D");
+  if (B * H * take == 0) return SI_OK;
+  SI_CHECK_ARG(k && v && page && page[0] && page[1], "si_page_write: NULL argument");
+  SI_CHECK_ARG(precision < SI_PREC_INT8 || (page[2] && page[3]), "si_page_write: NULL scales");
+  SI_CHECK_ARG(B * H < 65536 && B * H * capacity < ((int64_t)1 << 31),
+               "si_page_write: store too large for one launch");
+  Buckets pg = to_buckets(nullptr);
+  const int base = precision == SI_PREC_FP32 ? 0 : 4 * precision;
+  for (int j = 0; j < 4; ++j) pg.p[base + j] = page[j];
+  hipStream_t st = as_stream(stream);
+  const int es = dtype_size(dtype);
+  const int epl = 16 / es;
+  const int64_t lpr = D / epl;
+  const int64_t lpg = group / epl;
+  uintptr_t bits = reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v);
+  for (int j = 0; j < 4; ++j) bits |= reinterpret_cast<uintptr_t>(page[j]);
+  const bool fast = (bits & 15) == 0 && D % epl == 0 && pow2(lpr) && lpr >= 4 && lpr <= 64 &&
+                    group % epl == 0 && pow2(lpg) && lpg <= lpr && T < ((int64_t)1 << 31);
+  if (fast) {
+    const int rpb = (int)(256 / lpr);
+    const dim3 grid((unsigned)ceil_div(take, rpb), (unsigned)(B * H));
+#define SI_PW(DT_, L)                                                                         \
+  page_write_fast<DT_, L><<<grid, 256, 0, st>>>(k, v, (int)T, (int)t0, (int)take, (int)capacity, \
+                                               (int)offset, precision, (int)lpg, pg)
+#define SI_PW_DT(DT_)              \
+  switch (lpr) {                   \
+    case 4: SI_PW(DT_, 4); break;  \
+    case 8: SI_PW(DT_, 8); break;  \
+    case 16: SI_PW(DT_, 16); break; \
+    case 32: SI_PW(DT_, 32); break; \
+    default: SI_PW(DT_, 64); break; \
+  }
+    if (dtype == SI_DT_F32) { SI_PW_DT(SI_DT_F32) }
+    else if (dtype == SI_DT_F16) { SI_PW_DT(SI_DT_F16) }
+    else { SI_PW_DT(SI_DT_BF16) }
+#undef SI_PW_DT
+#undef SI_PW
+    return check_launch("si_page_write/fast");
+  }
+  const unsigned grid = grid_for(B * H * take, 256);
+  if (dtype == SI_DT_F32)
+    page_write_generic<SI_DT_F32><<<grid, 256, 0, st>>>(k, v, B * H, T, D, t0, take, capacity, offset, precision, group, pg);
+  else if (dtype == SI_DT_F16)
+    page_write_generic<SI_DT_F16><<<grid, 256, 0, st>>>(k, v, B * H, T, D, t0, take, capacity, offset, precision, group, pg);
+  else
+    page_write_generic<SI_DT_BF16><<<grid, 256, 0, st>>>(k, v, B * H, T, D, t0, take, capacity, offset, precision, group, pg);
+  return check_launch("si_page_write/generic");
+}
+
+extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, int64_t B,
+                              int64_t H, int64_t S, int64_t D, int64_t group, float* out_k,
+                              float* out_v, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_page_gather: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(n_pages >= 0 && B >= 0 && H >= 0 && S >= 0 && D > 0, "si_page_gather: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_page_gather: group must divide D");
+  if (n_pages == 0 || B * H == 0) return SI_OK;
+  SI_CHECK_ARG(table && out_k && out_v, "si_page_gather: NULL argument");
+  SI_CHECK_ARG(B * H < 65536 && n_pages < ((int64_t)1 << 31), "si_page_gather: too many pages");
+  const dim3 grid((unsigned)n_pages, (unsigned)(B * H));
+  // The vector path also needs aligned page rows: every page buffer is a
+  // fresh allocation and rows are D values long, so D % 4 == 0 keeps the 4-,
+  // 8- and 16-byte loads aligned.
+  const bool vec = D % 4 == 0 && group % 4 == 0 && D < (1 << 20) &&
+                   ((reinterpret_cast<uintptr_t>(out_k) | reinterpret_cast<uintptr_t>(out_v)) & 15) == 0;
+  hipStream_t st = as_stream(stream);
+#define SI_PG(SDT_)                                                                          \
+  do {                                                                                       \
+    if (vec) page_gather_kernel<SDT_, true><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);  \
+    else page_gather_kernel<SDT_, false><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);     \
+  } while (0)
+  if (dtype == SI_DT_F32) SI_PG(SI_DT_F32);
+  else if (dtype == SI_DT_F16) SI_PG(SI_DT_F16);
+  else SI_PG(SI_DT_BF16);
+#undef SI_PG
+  return check_launch("si_page_gather");
 }

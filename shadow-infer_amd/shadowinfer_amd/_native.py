@@ -47,6 +47,9 @@ _SIGNATURES = {
     "si_kv_pack": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "si_kv_pack_copy": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp]),
+    "si_page_write": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _vp,
+                             _i64, _i64, _vp]),
+    "si_page_gather": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_kv_unpack": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_kv_reuse": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                            _i64, _i32, _vp, _vp]),

@@ -5,6 +5,7 @@ packed-KV attention."""
 from .compress import compress_kv_with_plan
 from .packed_attention import packed_attention
 from .packed_kv_cache import PackedKVCache
+from .paged_kv_store import PagedKVStore
 from .rd_allocator import (
     admit_budget,
     admit_codes,
@@ -28,6 +29,7 @@ __all__ = [
     "PRECISION_CODES",
     "PRECISION_ORDER",
     "PackedKVCache",
+    "PagedKVStore",
     "PrecisionPlan",
     "admit_budget",
     "admit_codes",

@@ -38,6 +38,14 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in the header but not exported"
     assert sorted(_native.EXPORTED_SYMBOLS) == declared
+    # every extern "C" entry point defined in the sources is declared (and bound)
+    csrc = os.path.join(ROOT, "shadow-infer_amd", "csrc")
+    defined = set()
+    for f in os.listdir(csrc):
+        if f.endswith(".hip"):
+            defined |= set(re.findall(r'extern "C"[^(]*?\b(si_[a-z0-9_]+)\s*\(',
+                                      open(os.path.join(csrc, f)).read()))
+    assert defined == set(declared), sorted(defined ^ set(declared))
 
 
 def test_abi_version_and_status():
