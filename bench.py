@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -98,8 +99,13 @@ def bench_kv(torch, dev, steps, warmup):
         code, slot, table, sdt, group = cache.device_state()
         ok = torch.empty(B, H, S, D, dtype=torch.float32, device=dev)
         ov = torch.empty_like(ok)
+        flat = [plan.flat_indices[n] for n in ("fp32", "fp16", "int8", "int4")]
+        counts = (ctypes.c_int64 * 5)(*plan.counts)
+        # the raw pointer tables below stay valid while cache, plan and flat live in the dict
         layers.append(dict(k=k, v=v, code=code, slot=slot, table=table, sdt=sdt, cache=cache,
-                           ok=ok, ov=ov, packed=cache.memory_bytes()))
+                           plan=plan, flat_lists=flat, ok=ok, ov=ov,
+                           packed=cache.memory_bytes(), counts=counts,
+                           flat=_native.table4([f.data_ptr() for f in flat])))
     torch.cuda.synchronize()
 
     def pack(L):
@@ -107,8 +113,9 @@ def bench_kv(torch, dev, steps, warmup):
                      D, GROUP, L["code"].data_ptr(), L["slot"].data_ptr(), L["table"], sptr)
 
     def unpack(L):
-        _native.call("si_kv_unpack", L["code"].data_ptr(), L["slot"].data_ptr(), L["table"],
-                     L["sdt"], B, H, S, D, GROUP, L["ok"].data_ptr(), L["ov"].data_ptr(), sptr)
+        _native.call("si_kv_unpack_flat", L["code"].data_ptr(), L["slot"].data_ptr(), L["flat"],
+                     L["counts"], L["table"], L["sdt"], B, H, S, D, GROUP, L["ok"].data_ptr(),
+                     L["ov"].data_ptr(), sptr)
 
     def step():
         for L in layers:

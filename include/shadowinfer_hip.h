@@ -126,6 +126,18 @@ int si_kv_unpack(const int8_t* code, const int32_t* slot, const void* const* buc
                  int scale_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                  int64_t group, float* out_k, float* out_v, si_stream_t stream);
 
+/* si_kv_unpack in bucket order: flat = HOST array of 4 device int64 lists,
+ * flat[p][slot] = h*S + t of the entries of precision p in slot order (the
+ * plan's flat_indices, precision_plan.py:144-151, or si_plan_scatter);
+ * counts = HOST int64[5], entries per code 0..4 (summing to S*H). Each
+ * block decodes one precision and reads its bucket contiguously; entries of
+ * code 4 are written as zeros. Same output as si_kv_unpack (which it uses
+ * for shapes other than D in {64, 128} with 16-byte aligned outputs). */
+int si_kv_unpack_flat(const int8_t* code, const int32_t* slot, const int64_t* const* flat,
+                      const int64_t* counts, const void* const* buckets, int scale_dtype,
+                      int64_t B, int64_t H, int64_t S, int64_t D, int64_t group, float* out_k,
+                      float* out_v, si_stream_t stream);
+
 /* Replaces the copy loop of PackedKVCache.apply_reuse_mask
  * (packed_kv_cache.py:791-852). For each present entry (t,h) of the current
  * cache with mask[t*H+h] != 0: if t < S_prev and the previous cache holds it

@@ -743,47 +743,183 @@ __global__ __launch_bounds__(256) void kv_unpack_generic(const int8_t* __restric
 // Unpack for D in {64, 128}: blockIdx.y = b*H + h, blockIdx.x = tile of
 // RPP*U tokens; each thread dequantizes one 4-value chunk of U rows (all loads
 // issued before the stores) and writes 16-byte non-temporal stores.
+// Unpack of a 64-token tile of one (b, h), rows sorted by precision in LDS:
+// the tile's codes and slots are loaded once, one wave ranks the tokens per
+// code with ballots, and the block then decodes the rows in that order, so
+// runs of one precision share a wave while the tile's output (64 rows of D
+// floats, contiguous) is written with 16-byte stores.
 template <int D, int SDT, int U>
-__global__ __launch_bounds__(256) void kv_unpack_fast(const int8_t* __restrict__ code,
-                                                      const int32_t* __restrict__ slot, Buckets bk,
-                                                      int B, int H, int S, int g,
-                                                      float* __restrict__ ok,
-                                                      float* __restrict__ ov) {
-  constexpr int CPR = D / 4;      // 16-byte output chunks per row
-  constexpr int RPP = 256 / CPR;  // rows per pass of the block
-  const int ch = threadIdx.x % CPR;
-  const int sub = threadIdx.x / CPR;
+__global__ __launch_bounds__(256) void kv_unpack_sorted(const int8_t* __restrict__ code,
+                                                        const int32_t* __restrict__ slot,
+                                                        Buckets bk, int B, int H, int S, int g,
+                                                        float* __restrict__ ok,
+                                                        float* __restrict__ ov) {
+  constexpr int TT = 64;
+  constexpr int CPR = D / 4;      // 16-byte chunks per row
+  constexpr int RPP = 256 / CPR;  // rows per pass
+  __shared__ int s_tok[TT];
+  __shared__ int s_code[TT];
+  __shared__ int s_slot[TT];
   const int bh = blockIdx.y;
   const int h = bh % H;
   const int b = bh / H;
-  const int t0 = blockIdx.x * (RPP * U) + sub;
-  float4 rk[U], rv[U];
+  const int t0 = blockIdx.x * TT;
+  const int nt = min(TT, S - t0);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int c = SI_PREC_EVICTED, sl = 0;
+    if (lane < nt) {
+      const int e = (t0 + lane) * H + h;
+      c = code[e];
+      if (c < 0 || c > 3) c = SI_PREC_EVICTED;
+      else sl = slot[e];
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    int base = 0, pos = 0;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int t = t0 + u * RPP;
-    rk[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    rv[u] = rk[u];
-    if (t < S) {
-      const int e = t * H + h;
-      const int c = code[e];
-      if (c >= 0 && c <= 3) {
-        const int s = slot[e];
-        rk[u] = dequant4<SDT>(bk, 0, c, s, b, ch * 4, B, D, g);
-        rv[u] = dequant4<SDT>(bk, 1, c, s, b, ch * 4, B, D, g);
+    for (int p = 0; p <= SI_PREC_EVICTED; ++p) {
+      const uint64_t m = __ballot(lane < nt && c == p);
+      if (c == p) pos = base + __popcll(m & below);
+      base += __popcll(m);
+    }
+    if (lane < nt) {
+      s_tok[pos] = lane;
+      s_code[pos] = c;
+      s_slot[pos] = sl;
+    }
+  }
+  __syncthreads();
+  const int ch = threadIdx.x % CPR;
+  const int sub = threadIdx.x / CPR;
+  const int64_t row0 = (int64_t)bh * S + t0;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  for (int i0 = 0; i0 < nt; i0 += RPP * U) {
+    float4 rk[U], rv[U];
+    int tk[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * RPP + sub;
+      tk[u] = -1;
+      rk[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      rv[u] = rk[u];
+      if (i < nt) {
+        tk[u] = s_tok[i];
+        const int c = s_code[i];
+        const int sl = s_slot[i];
+        if (c == SI_PREC_FP16) {
+          rk[u] = dequant4<SDT>(bk, 0, SI_PREC_FP16, sl, b, ch * 4, B, D, g);
+          rv[u] = dequant4<SDT>(bk, 1, SI_PREC_FP16, sl, b, ch * 4, B, D, g);
+        } else if (c == SI_PREC_INT8) {
+          rk[u] = dequant4<SDT>(bk, 0, SI_PREC_INT8, sl, b, ch * 4, B, D, g);
+          rv[u] = dequant4<SDT>(bk, 1, SI_PREC_INT8, sl, b, ch * 4, B, D, g);
+        } else if (c == SI_PREC_INT4) {
+          rk[u] = dequant4<SDT>(bk, 0, SI_PREC_INT4, sl, b, ch * 4, B, D, g);
+          rv[u] = dequant4<SDT>(bk, 1, SI_PREC_INT4, sl, b, ch * 4, B, D, g);
+        } else if (c == SI_PREC_FP32) {
+          rk[u] = dequant4<SDT>(bk, 0, SI_PREC_FP32, sl, b, ch * 4, B, D, g);
+          rv[u] = dequant4<SDT>(bk, 1, SI_PREC_FP32, sl, b, ch * 4, B, D, g);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (tk[u] >= 0) {
+        const int64_t off = (row0 + tk[u]) * D + ch * 4;
+        __builtin_nontemporal_store(f32x4{rk[u].x, rk[u].y, rk[u].z, rk[u].w},
+                                    reinterpret_cast<f32x4*>(ok + off));
+        __builtin_nontemporal_store(f32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w},
+                                    reinterpret_cast<f32x4*>(ov + off));
       }
     }
   }
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  const int64_t row0 = (int64_t)bh * S;
+}
+
+// Unpack in bucket order (the order the buckets are stored in): block x
+// takes RPB consecutive rows (entry, b) of one precision's bucket, so every
+// wave decodes a single precision and reads the bucket contiguously; each
+// row goes to out row b*H*S + flat, flat = h*S + t from that precision's
+// flat index list (PrecisionPlan.flat_indices, precision_plan.py:144-151).
+// Blocks past the buckets zero the rows of entries whose code is outside
+// 0..3 (evicted or absent). blk_end[p]: first block after precision p's.
+struct UnpackLists {
+  const int64_t* flat[4];
+  int64_t n[4];
+  int64_t blk_end[5];
+};
+
+template <int D, int SDT, int U, int P>
+__device__ __forceinline__ void unpack_bucket_rows(const UnpackLists& L, const Buckets& bk,
+                                                   int64_t lb, int B, int64_t HS, int g,
+                                                   float* __restrict__ ok, float* __restrict__ ov) {
+  constexpr int CPR = D / 4;
+  constexpr int RPP = 256 / CPR;
+  const int ch = threadIdx.x % CPR;
+  const int64_t rows = L.n[P] * B;
+  const int64_t r0 = lb * (RPP * U) + threadIdx.x / CPR;
+  float4 rk[U], rv[U];
+  int64_t off[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int t = t0 + u * RPP;
-    if (t < S) {
-      const int64_t off = (row0 + t) * D + ch * 4;
+    const int64_t r = r0 + u * RPP;
+    off[u] = -1;
+    if (r < rows) {
+      const int64_t sl = r / B;
+      const int64_t b = r - sl * B;
+      off[u] = (b * HS + L.flat[P][sl]) * D + ch * 4;
+      rk[u] = dequant4<SDT>(bk, 0, P, sl, b, ch * 4, B, D, g);
+      rv[u] = dequant4<SDT>(bk, 1, P, sl, b, ch * 4, B, D, g);
+    }
+  }
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (off[u] >= 0) {
       __builtin_nontemporal_store(f32x4{rk[u].x, rk[u].y, rk[u].z, rk[u].w},
-                                  reinterpret_cast<f32x4*>(ok + off));
+                                  reinterpret_cast<f32x4*>(ok + off[u]));
       __builtin_nontemporal_store(f32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w},
-                                  reinterpret_cast<f32x4*>(ov + off));
+                                  reinterpret_cast<f32x4*>(ov + off[u]));
+    }
+  }
+}
+
+template <int D, int SDT, int U>
+__global__ __launch_bounds__(256) void kv_unpack_lists(UnpackLists L,
+                                                       const int8_t* __restrict__ code,
+                                                       Buckets bk, int B, int H, int S, int g,
+                                                       float* __restrict__ ok,
+                                                       float* __restrict__ ov) {
+  const int64_t blk = blockIdx.x;
+  const int64_t HS = (int64_t)H * S;
+  if (blk < L.blk_end[3]) {
+    if (blk < L.blk_end[0]) {
+      unpack_bucket_rows<D, SDT, U, SI_PREC_FP32>(L, bk, blk, B, HS, g, ok, ov);
+    } else if (blk < L.blk_end[1]) {
+      unpack_bucket_rows<D, SDT, U, SI_PREC_FP16>(L, bk, blk - L.blk_end[0], B, HS, g, ok, ov);
+    } else if (blk < L.blk_end[2]) {
+      unpack_bucket_rows<D, SDT, U, SI_PREC_INT8>(L, bk, blk - L.blk_end[1], B, HS, g, ok, ov);
+    } else {
+      unpack_bucket_rows<D, SDT, U, SI_PREC_INT4>(L, bk, blk - L.blk_end[2], B, HS, g, ok, ov);
+    }
+    return;
+  }
+  // zero rows: entries e = t*H + h with a code outside 0..3
+  constexpr int CPR = D / 4;
+  constexpr int RPP = 256 / CPR;
+  const int ch = threadIdx.x % CPR;
+  const int64_t e0 = (blk - L.blk_end[3]) * (RPP * U) + threadIdx.x / CPR;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t e = e0 + u * RPP;
+    if (e >= HS) break;
+    const int c = code[e];
+    if (c >= 0 && c <= 3) continue;
+    const int64_t t = e / H;
+    const int64_t h = e - t * H;
+    for (int b = 0; b < B; ++b) {
+      const int64_t o = (b * HS + h * S + t) * D + ch * 4;
+      __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f32x4*>(ok + o));
+      __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f32x4*>(ov + o));
     }
   }
 }
@@ -1176,24 +1312,20 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
 }
 
 template <int D>
-void launch_unpack_fast(int sdt, const int8_t* code, const int32_t* slot, const Buckets& bk,
-                        int64_t B, int64_t H, int64_t S, int64_t g, float* ok, float* ov,
-                        hipStream_t st) {
-  constexpr int U = 4;
-  constexpr int rpb = (256 / (D / 4)) * U;
-  const dim3 grid((unsigned)ceil_div(S, rpb), (unsigned)(B * H));
+void launch_unpack_sorted(int sdt, const int8_t* code, const int32_t* slot, const Buckets& bk,
+                          int64_t B, int64_t H, int64_t S, int64_t g, float* ok, float* ov,
+                          hipStream_t st) {
+  constexpr int U = 2;
+  const dim3 grid((unsigned)ceil_div(S, 64), (unsigned)(B * H));
   switch (sdt) {
     case SI_DT_F32:
-      kv_unpack_fast<D, SI_DT_F32, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S,
-                                                            (int)g, ok, ov);
+      kv_unpack_sorted<D, SI_DT_F32, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S, (int)g, ok, ov);
       break;
     case SI_DT_F16:
-      kv_unpack_fast<D, SI_DT_F16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S,
-                                                            (int)g, ok, ov);
+      kv_unpack_sorted<D, SI_DT_F16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S, (int)g, ok, ov);
       break;
     default:
-      kv_unpack_fast<D, SI_DT_BF16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H,
-                                                             (int)S, (int)g, ok, ov);
+      kv_unpack_sorted<D, SI_DT_BF16, U><<<grid, 256, 0, st>>>(code, slot, bk, (int)B, (int)H, (int)S, (int)g, ok, ov);
   }
 }
 
@@ -1266,9 +1398,9 @@ extern "C" int si_kv_unpack(const int8_t* code, const int32_t* slot, const void*
   const bool small = B * H < 65536 && S * H < ((int64_t)1 << 31) && group < ((int64_t)1 << 31);
   if (vec && small && (D == 128 || D == 64)) {
     if (D == 128)
-      launch_unpack_fast<128>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
+      launch_unpack_sorted<128>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
     else
-      launch_unpack_fast<64>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
+      launch_unpack_sorted<64>(scale_dtype, code, slot, bk, B, H, S, group, out_k, out_v, st);
     return check_launch("si_kv_unpack/fast");
   }
   if (vec) {
@@ -1421,4 +1553,62 @@ extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, 
   else SI_PG(SI_DT_BF16);
 #undef SI_PG
   return check_launch("si_page_gather");
+}
+
+extern "C" int si_kv_unpack_flat(const int8_t* code, const int32_t* slot,
+                                 const int64_t* const* flat, const int64_t* counts,
+                                 const void* const* buckets, int scale_dtype, int64_t B,
+                                 int64_t H, int64_t S, int64_t D, int64_t group, float* out_k,
+                                 float* out_v, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_unpack_flat: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0, "si_kv_unpack_flat: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_unpack_flat: group must divide D");
+  const int64_t total = B * H * S * D;
+  if (total == 0) return SI_OK;
+  SI_CHECK_ARG(code && slot && flat && counts && out_k && out_v && buckets,
+               "si_kv_unpack_flat: NULL argument");
+  int64_t nsum = 0;
+  for (int p = 0; p < 5; ++p) {
+    SI_CHECK_ARG(counts[p] >= 0, "si_kv_unpack_flat: negative count");
+    nsum += counts[p];
+  }
+  SI_CHECK_ARG(nsum == H * S, "si_kv_unpack_flat: counts sum to %lld, not S*H = %lld",
+               (long long)nsum, (long long)(H * S));
+  for (int p = 0; p < 4; ++p)
+    SI_CHECK_ARG(counts[p] == 0 || flat[p] != nullptr, "si_kv_unpack_flat: NULL flat list %d", p);
+  const bool vec = group % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(out_k) | reinterpret_cast<uintptr_t>(out_v)) & 15) == 0;
+  const bool small = B * H * S < ((int64_t)1 << 31) && B < ((int64_t)1 << 31);
+  if (!(vec && small && (D == 128 || D == 64)))  // other shapes: the token-order kernels
+    return si_kv_unpack(code, slot, buckets, scale_dtype, B, H, S, D, group, out_k, out_v, stream);
+  const Buckets bk = to_buckets(buckets);
+  constexpr int U = 4;
+  const int64_t rpb = (256 / (D / 4)) * U;
+  UnpackLists L;
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    L.flat[p] = flat[p];
+    L.n[p] = counts[p];
+    acc += ceil_div(counts[p] * B, rpb);
+    L.blk_end[p] = acc;
+  }
+  L.blk_end[4] = acc + (counts[4] > 0 ? ceil_div(H * S, rpb) : 0);
+  SI_CHECK_ARG(L.blk_end[4] < ((int64_t)1 << 31), "si_kv_unpack_flat: too many blocks");
+  if (L.blk_end[4] == 0) return SI_OK;
+  const dim3 grid((unsigned)L.blk_end[4]);
+  hipStream_t st = as_stream(stream);
+#define SI_UL(D_, SDT_) \
+  kv_unpack_lists<D_, SDT_, U><<<grid, 256, 0, st>>>(L, code, bk, (int)B, (int)H, (int)S, (int)group, out_k, out_v)
+  if (D == 128) {
+    if (scale_dtype == SI_DT_F32) SI_UL(128, SI_DT_F32);
+    else if (scale_dtype == SI_DT_F16) SI_UL(128, SI_DT_F16);
+    else SI_UL(128, SI_DT_BF16);
+  } else {
+    if (scale_dtype == SI_DT_F32) SI_UL(64, SI_DT_F32);
+    else if (scale_dtype == SI_DT_F16) SI_UL(64, SI_DT_F16);
+    else SI_UL(64, SI_DT_BF16);
+  }
+#undef SI_UL
+  return check_launch("si_kv_unpack_flat");
 }

@@ -21,6 +21,7 @@ RuntimeError (this build has no CPU implementation of the data plane).
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any, Dict, List, Optional, Set, Tuple, Union
 
 import numpy as np
@@ -209,10 +210,14 @@ class PackedKVCache:
         k_out = torch.empty(shape, dtype=torch.float32, device=dev)
         v_out = torch.empty(shape, dtype=torch.float32, device=dev)
         if k_out.numel():
-            _native.call("si_kv_unpack", self._grouping.code.data_ptr(),
-                         self._grouping.slot.data_ptr(), self._bucket_table(),
-                         _native.dtype_code(self._scale_dtype), *shape, self._group_size,
-                         k_out.data_ptr(), v_out.data_ptr(), _native.stream(dev))
+            gr = self._grouping
+            flat = gr.flat_lists(self.seq_len, self.num_heads)
+            counts = (ctypes.c_int64 * 5)(*[int(c) for c in gr.counts])
+            _native.call("si_kv_unpack_flat", gr.code.data_ptr(), gr.slot.data_ptr(),
+                         _native.table4([f.data_ptr() for f in flat]), counts,
+                         self._bucket_table(), _native.dtype_code(self._scale_dtype), *shape,
+                         self._group_size, k_out.data_ptr(), v_out.data_ptr(),
+                         _native.stream(dev))
         return k_out, v_out
 
     def unpack_reference(self) -> Tuple[torch.Tensor, torch.Tensor]:

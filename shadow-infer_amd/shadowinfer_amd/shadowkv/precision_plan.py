@@ -69,15 +69,30 @@ class DeviceGrouping:
 
     ``code``: int8 [S*H] sanitized codes (absent/unknown -> 4);
     ``slot``: int32 [S*H] bucket positions (-1 if absent);
-    ``counts``: entries per code 0..4 (host ints).
+    ``counts``: entries per code 0..4 (host ints);
+    ``flat``: per precision, int64 ``h*S + t`` of the bucket's entries in
+    slot order (the plan's ``flat_indices``), built on first use.
     """
 
-    __slots__ = ("code", "slot", "counts")
+    __slots__ = ("code", "slot", "counts", "flat")
 
-    def __init__(self, code: torch.Tensor, slot: torch.Tensor, counts: List[int]):
+    def __init__(self, code: torch.Tensor, slot: torch.Tensor, counts: List[int],
+                 flat: Optional[List[torch.Tensor]] = None):
         self.code = code
         self.slot = slot
         self.counts = counts
+        self.flat = flat
+
+    def flat_lists(self, S: int, H: int) -> List[torch.Tensor]:
+        """Per-precision ``h*S + t`` lists in slot order (si_plan_scatter)."""
+        if self.flat is None:
+            dev = self.code.device
+            flat = [torch.empty(self.counts[p], dtype=torch.long, device=dev) for p in range(4)]
+            _native.call("si_plan_scatter", self.code.data_ptr(), self.slot.data_ptr(), S, H,
+                         _native.table4([f.data_ptr() for f in flat]), _native.table4([None] * 4),
+                         _native.stream(dev))
+            self.flat = flat
+        return self.flat
 
     @staticmethod
     def scan(codes_flat: torch.Tensor, evict_mask: Optional[torch.Tensor] = None) -> "DeviceGrouping":
@@ -176,6 +191,7 @@ class PrecisionPlan:
                      _native.table4([flat_indices[n].data_ptr() for n in PRECISION_ORDER]),
                      _native.table4([entries[n].data_ptr() for n in PRECISION_ORDER]),
                      _native.stream(device))
+        grouping.flat = [flat_indices[n] for n in PRECISION_ORDER]
         return cls(seq_len, num_heads, codes, flat_indices, reuse_entries, reuse_flat,
                    grouping=grouping, entries=entries)
 

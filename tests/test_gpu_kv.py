@@ -163,6 +163,31 @@ def test_pack_is_deterministic(dev):
             assert (ta is None and tb is None) or torch.equal(ta, tb)
 
 
+# ------------------------------------------------------------ unpack routes
+@pytest.mark.parametrize("dtype,B,H,S,D", [(torch.bfloat16, 1, 32, 1000, 128),
+                                           (torch.float32, 2, 3, 77, 64),
+                                           (torch.float16, 2, 5, 130, 128)])
+def test_unpack_token_and_bucket_order_agree(dev, dtype, B, H, S, D):
+    """si_kv_unpack (64-token tiles sorted by precision) and si_kv_unpack_flat
+    (bucket order, used by PackedKVCache.unpack) against the oracle, with
+    evicted entries and every precision present."""
+    from shadowinfer_amd import _native
+    k, v = kv_inputs(B, H, S, D, dtype, seed=S + D)
+    codes = mixed_codes(S, H, seed=S, probs=(1, 2, 3, 3), sink=2, evicted=0.1)
+    cache = _pack(k, v, codes, dev)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
+    fk, fv = cache.unpack()
+    np.testing.assert_array_equal(fk.cpu().numpy(), rk)
+    np.testing.assert_array_equal(fv.cpu().numpy(), rv)
+    code, slot, table, sdt, group = cache.device_state()
+    tk = torch.empty(B, H, S, D, dtype=torch.float32, device=dev)
+    tv = torch.empty_like(tk)
+    _native.call("si_kv_unpack", code.data_ptr(), slot.data_ptr(), table, sdt, B, H, S, D, group,
+                 tk.data_ptr(), tv.data_ptr(), _native.stream(dev))
+    np.testing.assert_array_equal(tk.cpu().numpy(), rk)
+    np.testing.assert_array_equal(tv.cpu().numpy(), rv)
+
+
 # --------------------------------------------------------------------- evict
 def test_evict_config1(dev):
     """Config-1 eviction: the 25% lowest-importance token-heads (stable
