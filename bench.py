@@ -109,8 +109,9 @@ def bench_kv(torch, dev, steps, warmup):
     torch.cuda.synchronize()
 
     def pack(L):
-        _native.call("si_kv_pack", L["k"].data_ptr(), L["v"].data_ptr(), _native.DT_BF16, B, H, S,
-                     D, GROUP, L["code"].data_ptr(), L["slot"].data_ptr(), L["table"], sptr)
+        _native.call("si_kv_pack_flat", L["k"].data_ptr(), L["v"].data_ptr(), _native.DT_BF16, B,
+                     H, S, D, GROUP, L["code"].data_ptr(), L["slot"].data_ptr(), L["flat"],
+                     L["counts"], L["table"], sptr)
 
     def unpack(L):
         _native.call("si_kv_unpack_flat", L["code"].data_ptr(), L["slot"].data_ptr(), L["flat"],

@@ -104,6 +104,16 @@ int si_kv_pack(const void* k, const void* v, int dtype, int64_t B, int64_t H, in
                int64_t D, int64_t group, const int8_t* code, const int32_t* slot,
                void* const* buckets, si_stream_t stream);
 
+/* si_kv_pack in bucket order: flat = HOST array of 4 device int64 lists
+ * (flat[p][slot] = h*S + t, the plan's flat_indices), counts = HOST int64[5]
+ * (entries per code 0..4, summing to S*H). Each block quantizes one
+ * precision and writes its bucket rows contiguously. Same buckets as
+ * si_kv_pack (which it uses for shapes the row kernels do not cover). */
+int si_kv_pack_flat(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+                    int64_t D, int64_t group, const int8_t* code, const int32_t* slot,
+                    const int64_t* const* flat, const int64_t* counts, void* const* buckets,
+                    si_stream_t stream);
+
 /* Fused form of ShadowKVAgent._compress_kv_with_plan
  * (shadowinfer/shadowkv/shadowkv_agent.py:1698-1809) and si_kv_pack: one
  * pass over K/V writes the buckets (as si_kv_pack) and the dense working

@@ -168,6 +168,14 @@ __device__ __forceinline__ void store_i4(uint8_t* dst, const float* q) {
 // int8/int4 -> the integer codes (not dequantized), other codes -> 0; entries
 // flagged in `reuse` take the rows of the previous K/V instead.
 // ---------------------------------------------------------------------------
+// Per-precision flat index lists (h*S + t in slot order, the plan's
+// flat_indices) and the block ranges of a bucket-order launch.
+struct UnpackLists {
+  const int64_t* flat[4];
+  int64_t n[4];
+  int64_t blk_end[5];
+};
+
 struct WorkCopy {
   void* k;
   void* v;
@@ -601,6 +609,89 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
   }
 }
 
+// Pack in bucket order: block x takes RPP*U consecutive rows (entry, b) of
+// one precision's bucket (the flat index lists give each row's dense row
+// b*H*S + h*S + t), so every wave quantizes a single precision and the bucket
+// rows are written contiguously. blk_end[p]: first block after precision p's.
+template <int DT, int LPR, int U, int P>
+__device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
+                                                 const void* __restrict__ vin,
+                                                 const UnpackLists& L, int64_t lb, int B,
+                                                 int64_t HS, int lpg, const Buckets& bk) {
+  constexpr int EPL = Chunk<DT>::EPL;
+  constexpr int D = EPL * LPR;
+  constexpr int RPP = 256 / LPR;
+  const int lane = threadIdx.x % LPR;
+  const int64_t rows = L.n[P] * B;
+  const int64_t r0 = lb * (RPP * U) + threadIdx.x / LPR;
+  if constexpr (DT == SI_DT_BF16) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    uint32_t wk[U][4], wv[U][4];
+    int64_t sl[U], bb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * RPP;
+      sl[u] = -1;
+      if (r < rows) {
+        sl[u] = r / B;
+        bb[u] = r - sl[u] * B;
+        const int64_t off = ((bb[u] * HS + L.flat[P][sl[u]]) * D + lane * EPL) * 2;
+        const u32x4 a = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + off));
+        const u32x4 b = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vin) + off));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wk[u][i] = a[i];
+          wv[u][i] = b[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (sl[u] >= 0)
+        pack_row_bf16<LPR, false>(wk[u], wv[u], P, (int)sl[u], (int)bb[u], B, lane, lpg, bk,
+                                  nullptr, nullptr);
+  } else {
+    float xk[U][EPL], xv[U][EPL];
+    int64_t sl[U], bb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * RPP;
+      sl[u] = -1;
+      if (r < rows) {
+        sl[u] = r / B;
+        bb[u] = r - sl[u] * B;
+        const int64_t el = (bb[u] * HS + L.flat[P][sl[u]]) * D + lane * EPL;
+        load_chunk<DT>(kin, el, xk[u]);
+        load_chunk<DT>(vin, el, xv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (sl[u] >= 0)
+        pack_row<DT, LPR, false>(xk[u], xv[u], P, (int)sl[u], (int)bb[u], B, lane, lpg, bk,
+                                 nullptr, nullptr);
+  }
+}
+
+template <int DT, int LPR, int U>
+__global__ __launch_bounds__(256) void kv_pack_lists(const void* __restrict__ kin,
+                                                     const void* __restrict__ vin, UnpackLists L,
+                                                     int B, int H, int S, int lpg, Buckets bk) {
+  const int64_t blk = blockIdx.x;
+  const int64_t HS = (int64_t)H * S;
+  if (blk < L.blk_end[0]) {
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP32>(kin, vin, L, blk, B, HS, lpg, bk);
+  } else if (blk < L.blk_end[1]) {
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP16>(kin, vin, L, blk - L.blk_end[0], B, HS, lpg, bk);
+  } else if (blk < L.blk_end[2]) {
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT8>(kin, vin, L, blk - L.blk_end[1], B, HS, lpg, bk);
+  } else {
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT4>(kin, vin, L, blk - L.blk_end[2], B, HS, lpg, bk);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Generic pack: one thread per entry, any B, D, group (odd sizes included).
 // ---------------------------------------------------------------------------
@@ -841,11 +932,6 @@ __global__ __launch_bounds__(256) void kv_unpack_sorted(const int8_t* __restrict
 // flat index list (PrecisionPlan.flat_indices, precision_plan.py:144-151).
 // Blocks past the buckets zero the rows of entries whose code is outside
 // 0..3 (evicted or absent). blk_end[p]: first block after precision p's.
-struct UnpackLists {
-  const int64_t* flat[4];
-  int64_t n[4];
-  int64_t blk_end[5];
-};
 
 template <int D, int SDT, int U, int P>
 __device__ __forceinline__ void unpack_bucket_rows(const UnpackLists& L, const Buckets& bk,
@@ -1611,4 +1697,66 @@ extern "C" int si_kv_unpack_flat(const int8_t* code, const int32_t* slot,
   }
 #undef SI_UL
   return check_launch("si_kv_unpack_flat");
+}
+
+extern "C" int si_kv_pack_flat(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                               int64_t S, int64_t D, int64_t group, const int8_t* code,
+                               const int32_t* slot, const int64_t* const* flat,
+                               const int64_t* counts, void* const* buckets, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_kv_pack_flat: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0, "si_kv_pack_flat: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_pack_flat: group must divide D");
+  SI_CHECK_ARG(buckets != nullptr && flat != nullptr && counts != nullptr,
+               "si_kv_pack_flat: NULL table");
+  if (B * H * S == 0) return SI_OK;
+  int64_t nsum = 0;
+  for (int p = 0; p < 5; ++p) {
+    SI_CHECK_ARG(counts[p] >= 0, "si_kv_pack_flat: negative count");
+    nsum += counts[p];
+  }
+  SI_CHECK_ARG(nsum == H * S, "si_kv_pack_flat: counts sum to %lld, not S*H = %lld",
+               (long long)nsum, (long long)(H * S));
+  for (int p = 0; p < 4; ++p)
+    SI_CHECK_ARG(counts[p] == 0 || flat[p] != nullptr, "si_kv_pack_flat: NULL flat list %d", p);
+  const Buckets bk = to_buckets(buckets);
+  hipStream_t st = as_stream(stream);
+  const int es = dtype_size(dtype);
+  const int epl = 16 / es;
+  const int64_t lpr = D / epl;
+  const int64_t lpg = group / epl;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
+  const bool fast = aligned && D % epl == 0 && pow2(lpr) && lpr >= 4 && lpr <= 64 &&
+                    group % epl == 0 && pow2(lpg) && lpg <= lpr && B * H * S < ((int64_t)1 << 31);
+  if (!fast) return si_kv_pack(k, v, dtype, B, H, S, D, group, code, slot, buckets, stream);
+  constexpr int U = 2;
+  const int64_t rpb = (256 / lpr) * U;
+  UnpackLists L;
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    L.flat[p] = flat[p];
+    L.n[p] = counts[p];
+    acc += ceil_div(counts[p] * B, rpb);
+    L.blk_end[p] = acc;
+  }
+  L.blk_end[4] = acc;
+  if (acc == 0) return SI_OK;
+  SI_CHECK_ARG(acc < ((int64_t)1 << 31), "si_kv_pack_flat: too many blocks");
+  const dim3 grid((unsigned)acc);
+#define SI_PL(DT_, L_) \
+  kv_pack_lists<DT_, L_, U><<<grid, 256, 0, st>>>(k, v, L, (int)B, (int)H, (int)S, (int)lpg, bk)
+#define SI_PL_DT(DT_)               \
+  switch (lpr) {                    \
+    case 4: SI_PL(DT_, 4); break;   \
+    case 8: SI_PL(DT_, 8); break;   \
+    case 16: SI_PL(DT_, 16); break; \
+    case 32: SI_PL(DT_, 32); break; \
+    default: SI_PL(DT_, 64); break; \
+  }
+  if (dtype == SI_DT_F32) { SI_PL_DT(SI_DT_F32) }
+  else if (dtype == SI_DT_F16) { SI_PL_DT(SI_DT_F16) }
+  else { SI_PL_DT(SI_DT_BF16) }
+#undef SI_PL_DT
+#undef SI_PL
+  return check_launch("si_kv_pack_flat");
 }

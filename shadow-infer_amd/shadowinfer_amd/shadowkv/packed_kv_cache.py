@@ -115,9 +115,12 @@ class PackedKVCache:
         self._buckets = self._alloc_buckets(grouping.counts, dev, k.dtype)
         self._view = None
         if work_copy is None:
-            _native.call("si_kv_pack", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,
-                         grouping.code.data_ptr(), grouping.slot.data_ptr(), self._bucket_table(),
-                         _native.stream(dev))
+            flat = grouping.flat_lists(S, H)
+            counts = (ctypes.c_int64 * 5)(*[int(c) for c in grouping.counts])
+            _native.call("si_kv_pack_flat", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,
+                         grouping.code.data_ptr(), grouping.slot.data_ptr(),
+                         _native.table4([f.data_ptr() for f in flat]), counts,
+                         self._bucket_table(), _native.stream(dev))
         else:
             out_k, out_v, k_prev, v_prev, reuse = work_copy
             _native.call("si_kv_pack_copy", k.data_ptr(), v.data_ptr(), dt, B, H, S, D, g,

@@ -180,6 +180,20 @@ def test_unpack_token_and_bucket_order_agree(dev, dtype, B, H, S, D):
     np.testing.assert_array_equal(fk.cpu().numpy(), rk)
     np.testing.assert_array_equal(fv.cpu().numpy(), rv)
     code, slot, table, sdt, group = cache.device_state()
+    # token-order pack through the ABI into a second set of buckets: same bytes
+    from shadowinfer_amd.shadowkv.packed_kv_cache import PackedKVCache as _P
+    other = _P(B, H, S, D, device=dev)
+    other._group_size, other._scale_dtype, other._grouping = group, dtype, cache._grouping
+    other._buckets = other._alloc_buckets(cache._grouping.counts, dev, dtype)
+    kd, vd = k.to(dev), v.to(dev)
+    _native.call("si_kv_pack", kd.data_ptr(), vd.data_ptr(), _native.dtype_code(dtype),
+                 B, H, S, D, group, code.data_ptr(), slot.data_ptr(), other._bucket_table(),
+                 _native.stream(dev))
+    torch.cuda.synchronize(dev)
+    for name, d in cache.packed_data.items():
+        for key in ("k", "v", "scale_k", "scale_v"):
+            if d[key] is not None:
+                assert torch.equal(d[key], other.packed_data[name][key]), (name, key)
     tk = torch.empty(B, H, S, D, dtype=torch.float32, device=dev)
     tv = torch.empty_like(tk)
     _native.call("si_kv_unpack", code.data_ptr(), slot.data_ptr(), table, sdt, B, H, S, D, group,
