@@ -19,7 +19,7 @@ and the CPU baseline (the oracle on the host, a bounded sample of the same
 workload).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--part all|kv|gemm|attention|admit|paged|calib]
+                       [--part all|kv|gemm|attention|admit|paged|step|calib]
 """
 
 from __future__ import annotations
@@ -401,6 +401,74 @@ def bench_paged(torch, dev, iters=10):
     return res
 
 
+def bench_step(torch, dev, steps=8, warmup=2, gen_steps=64):
+    """One denoising step of a random-init Llama-7B-shaped diffusion LM
+    (32 layers, hidden 4096, 32 heads, SwiGLU 11008, vocab 32000) on B=1,
+    S=2048 with 50% mask tokens: INT8 gate|up and down projections, per-layer
+    packed KV rebuilt every step (codes 25% fp16 / 50% int8 / 25% int4 g16,
+    4-token fp16 sink), step reuse on every other layer after the first step,
+    one unmasking round per step. Reports the steady-state step (16 computed +
+    16 reused layers), a step with every layer computed, and a whole
+    64-step generation."""
+    import numpy as np
+    from shadowinfer_amd.execution import (DiffusionLlamaShape, PackedDiffusionLlama,
+                                           StepReuseConfig, StepReuseState, mask_tokens)
+    from shadowinfer_amd.shadowkv import PrecisionPlan
+
+    cfg = DiffusionLlamaShape()
+    Sd = 2048
+    model = PackedDiffusionLlama(cfg, device=dev, seed=5)
+    plans = []
+    for i in range(cfg.num_hidden_layers):
+        rng = np.random.default_rng(100 + i)
+        codes = rng.choice(np.array([1, 2, 3], np.int8), size=(Sd, cfg.num_attention_heads),
+                           p=[0.25, 0.5, 0.25])
+        codes[:4, :] = 1
+        plans.append(PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev)))
+    reuse_cfg = StepReuseConfig(enabled=True, threshold=float("inf"), warmup_steps=1,
+                                reusable_layers=set(range(1, cfg.num_hidden_layers, 2)))
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    res = {}
+
+    def fresh():
+        tokens, masked = mask_tokens(1, Sd, 0.5, cfg, dev, seed=7)
+        return tokens, masked, StepReuseState()
+
+    # every layer computed (no reuse state)
+    tokens, masked, _ = fresh()
+    for _ in range(warmup):
+        model.forward_step(tokens, plans)
+    res["full_step_ms"] = timer.time(lambda: model.forward_step(tokens, plans), steps)
+
+    # steady state: step >= 1 with half the layers reused
+    tokens, masked, state = fresh()
+    model.denoise_step(tokens, masked, plans, 0, 0.9, state, reuse_cfg)
+    it = iter(range(1, 10 ** 6))
+    for _ in range(warmup):
+        model.denoise_step(tokens, masked, plans, next(it), 0.9, state, reuse_cfg)
+    res["step_ms"] = timer.time(
+        lambda: model.denoise_step(tokens, masked, plans, next(it), 0.9, state, reuse_cfg), steps)
+    res["reused_ratio"] = state.stats()["reused_ratio"]
+
+    # a whole generation: step 0 computes every layer, then 63 reuse steps
+    tokens, masked, state = fresh()
+    n_masked = int(masked.sum())
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for step in range(gen_steps):
+        model.denoise_step(tokens, masked, plans, step, 0.9, state, reuse_cfg)
+    end.record(stream)
+    end.synchronize()
+    res["generation_ms"] = start.elapsed_time(end)
+    res["generation_steps"] = gen_steps
+    res["unmasked_in_generation"] = n_masked - int(masked.sum())
+    res["positions_per_s"] = Sd / (res["step_ms"] * 1e-3)
+    return res
+
+
 def cpu_baseline(layers: int = 4):
     """The oracle (C + numpy, one thread) on ``layers`` of the same layers:
     pack + unpack, algorithmic bytes / wall time."""
@@ -453,7 +521,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="same as --part kv")
     ap.add_argument("--part", choices=("all", "kv", "gemm", "attention", "admit", "paged",
-                                       "calib"),
+                                       "step", "calib"),
                     default="all",
                     help="run one part only (for profiling); 'calib' runs the plain device "
                          "fill and copy that calibrate the HBM byte counters")
@@ -482,16 +550,16 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "fill + 3 copies", "bytes": CALIB_BYTES}), flush=True)
         return
-    if args.part in ("gemm", "attention", "admit", "paged"):
+    if args.part in ("gemm", "attention", "admit", "paged", "step"):
         fn = {"gemm": bench_gemm, "attention": bench_attention, "admit": bench_admit,
-              "paged": bench_paged}[args.part]
+              "paged": bench_paged, "step": bench_step}[args.part]
         log(args.part)
         print(json.dumps({args.part: fn(torch, dev)}), flush=True)
         return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
     log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
-    gemm = attn = adm = paged = None
+    gemm = attn = adm = paged = step = None
     if args.part == "all":
         log("int8 gemm")
         gemm = bench_gemm(torch, dev)
@@ -501,6 +569,8 @@ def main():
         adm = bench_admit(torch, dev, with_cpu=not args.no_cpu)
         log("paged store")
         paged = bench_paged(torch, dev)
+        log("denoising step")
+        step = bench_step(torch, dev)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle)")
@@ -557,6 +627,12 @@ def main():
         line["admission"] = {"shape": "S=8192 x H=32 token-heads, B=1, D=128, bf16 K/V",
                              **{k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in adm.items()}}
+    if step is not None:
+        line["denoising_step"] = {
+            "shape": "Llama-7B-shaped diffusion LM, 32 layers, hidden 4096, 32 heads, SwiGLU 11008, "
+                     "vocab 32000, B=1, S=2048, 50% masks, INT8 gate|up/down, packed KV per layer "
+                     "(replace), reuse on every other layer",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in step.items()}}
     print(json.dumps(line), flush=True)
 
 

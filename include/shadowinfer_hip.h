@@ -186,6 +186,15 @@ int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t
                        int64_t group, float sm_scale, void* out, int out_dtype,
                        void* workspace, size_t workspace_bytes, si_stream_t stream);
 
+/* si_attn_packed_fwd writing token-major out [B, S_q, H, D]: the
+ * attn.transpose(1, 2).reshape(B, S, H * D) layout the output projection
+ * reads (shadowinfer/models/diffusion_llama.py:390-391). */
+int si_attn_packed_fwd_tokens(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
+                              int64_t D, const int8_t* code, const int32_t* slot,
+                              const void* const* buckets, int scale_dtype, int64_t S_kv,
+                              int64_t group, float sm_scale, void* out, int out_dtype,
+                              void* workspace, size_t workspace_bytes, si_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Quantizer                                                               */
 /* ---------------------------------------------------------------------- */
@@ -323,6 +332,43 @@ int si_admit_codes(const int8_t* codes, int8_t* out_codes, int64_t S, int64_t H,
                    const uint8_t* protected_mask, int64_t sink_tokens, int64_t budget_bytes,
                    int use_budget, int allow_eviction, const int64_t* costs, int64_t* result,
                    void* workspace, size_t workspace_bytes, si_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Denoising step of a Llama-shaped diffusion LM (row kernels)             */
+/* ---------------------------------------------------------------------- */
+
+/* DiffusionLlamaRMSNorm (shadowinfer/models/diffusion_llama.py:311-321) over
+ * rows of K (K % 8 == 0, K <= 16384): y = T((x / sqrt(mean(x^2) + eps)) * w)
+ * with fp32 arithmetic and one rounding to T = dtype. x [M, K], weight [K] in
+ * dtype. Outputs (each optional, at least one): y [M, K] in dtype; q int8
+ * [M, K] + scale fp32 [M], the INT8Linear activation quantization of y
+ * (shadowinfer/ffn_optimizer/int8_linear.py:96-98), identical to
+ * si_act_quant_i8 on y. */
+int si_rmsnorm_rows(const void* x, int dtype, int64_t M, int64_t K, const void* weight,
+                    float eps, void* y, int8_t* q, float* scale, si_stream_t stream);
+
+/* RoPE and head split of DiffusionLlamaAttention.forward
+ * (shadowinfer/models/diffusion_llama.py:362-373): qkv [B*S, 3*H*D] (q | k | v)
+ * -> q, k, v [B, H, S, D]; q and k rotated with the rotate-half tables
+ * cos_table, sin_table [S, D] (diffusion_llama.py:505-514), fp32 arithmetic,
+ * one rounding. D = 64 or 128; all pointers 16-byte aligned. */
+int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+                  const void* cos_table, const void* sin_table, void* q, void* k, void* v,
+                  si_stream_t stream);
+
+/* DiffusionLlamaMLP's silu(gate) * up (shadowinfer/models/diffusion_llama.py:332-333)
+ * and the down INT8Linear's activation quantization (int8_linear.py:96-98):
+ * gate_up [M, 2F] (gate | up) in dtype; h = T(T(silu(g)) * u) [M, F]
+ * (optional), q int8 [M, F], scale fp32 [M]. F % 8 == 0, F <= 16384. */
+int si_swiglu_quant(const void* gate_up, int dtype, int64_t M, int64_t F, void* h, int8_t* q,
+                    float* scale, si_stream_t stream);
+
+/* Per-position argmax and confidence of schedule_round
+ * (shadowinfer/execution/block_decoding.py:148-151): tokens[m] = first index of
+ * the largest logit of row m (NaN counts as largest); confidence[m] = the max
+ * softmax probability 1 / sum_v exp(l_v - l_max), fp32. logits [M, V]. */
+int si_row_argmax_conf(const void* logits, int dtype, int64_t M, int64_t V, int64_t* tokens,
+                       float* confidence, si_stream_t stream);
 
 #ifdef __cplusplus
 }

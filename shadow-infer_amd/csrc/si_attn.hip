@@ -226,11 +226,16 @@ __device__ __forceinline__ _Float16 exact_h(float s, float qmax) {
 // Evicted/absent keys have score 0; they are added to the softmax
 // denominator at the end (n_ev * 2^(0 - m)).
 // ---------------------------------------------------------------------------
+// Output element strides of b, h and the query index (the head dim is unit stride).
+struct OutStrides {
+  int64_t b, h, s;
+};
+
 template <int D, int SDT, int QDT>
 __global__ __launch_bounds__(512) void attn_packed_fwd(
     const uint16_t* __restrict__ Q, int64_t B, int64_t H, int64_t Sq, int64_t cap,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ lists, Buckets bk, int64_t g,
-    float scale_log2, void* __restrict__ O, int odt) {
+    float scale_log2, void* __restrict__ O, int odt, OutStrides os) {
   using C = AttnCfg<D>;
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DB = D / 32;  // 32-row blocks of O^T
@@ -644,7 +649,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 
   if (!m_ok) return;
   const float inv = 1.0f / l_run;
-  const int64_t obase = ((b * H + h) * Sq + m) * D;
+  const int64_t obase = b * os.b + h * os.h + m * os.s;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -670,20 +675,21 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 template <int D, int QDT>
 void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t B, int64_t H,
                  int64_t Sq, int64_t cap, const int32_t* counts, const int32_t* lists,
-                 const Buckets& bk, int64_t g, float scale_log2, void* out, int odt) {
+                 const Buckets& bk, int64_t g, float scale_log2, void* out, int odt,
+                 const OutStrides& os) {
   constexpr int NT = 64 * AttnCfg<D>::NW;
   switch (sdt) {
     case SI_DT_F32:
       attn_packed_fwd<D, SI_DT_F32, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
-                                                              g, scale_log2, out, odt);
+                                                              g, scale_log2, out, odt, os);
       break;
     case SI_DT_F16:
       attn_packed_fwd<D, SI_DT_F16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
-                                                              g, scale_log2, out, odt);
+                                                              g, scale_log2, out, odt, os);
       break;
     default:
       attn_packed_fwd<D, SI_DT_BF16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
-                                                               bk, g, scale_log2, out, odt);
+                                                               bk, g, scale_log2, out, odt, os);
   }
 }
 
@@ -697,12 +703,11 @@ extern "C" size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv) {
   return (size_t)H * 8 * sizeof(int32_t) + (size_t)H * (size_t)list_cap(S_kv) * sizeof(int32_t);
 }
 
-extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
-                                  int64_t D, const int8_t* code, const int32_t* slot,
-                                  const void* const* buckets, int scale_dtype, int64_t S_kv,
-                                  int64_t group, float sm_scale, void* out, int out_dtype,
-                                  void* workspace, size_t workspace_bytes, si_stream_t stream) {
-  clear_error();
+namespace {
+int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int64_t D,
+             const int8_t* code, const int32_t* slot, const void* const* buckets, int scale_dtype,
+             int64_t S_kv, int64_t group, float sm_scale, void* out, int out_dtype,
+             const OutStrides& os, void* workspace, size_t workspace_bytes, hipStream_t st) {
   SI_CHECK_ARG(q_dtype == SI_DT_BF16 || q_dtype == SI_DT_F16,
                "si_attn_packed_fwd: q dtype must be bf16 or fp16 (got %d)", q_dtype);
   SI_CHECK_ARG(dtype_ok(scale_dtype), "si_attn_packed_fwd: unsupported scale dtype %d",
@@ -729,7 +734,6 @@ extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t
   const int64_t cap = list_cap(S_kv);
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
   int32_t* lists = counts + H * 8;
-  hipStream_t st = as_stream(stream);
   attn_lists<<<(unsigned)H, 256, 0, st>>>(code, slot, H, S_kv, cap, counts, lists);
   if (int rc = check_launch("si_attn_packed_fwd")) return rc;
   const int64_t bmq = D == 128 ? AttnCfg<128>::BMQ : AttnCfg<64>::BMQ;
@@ -739,17 +743,42 @@ extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t
   if (D == 128) {
     if (q_dtype == SI_DT_BF16)
       launch_attn<128, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                   group, scale_log2, out, out_dtype);
+                                   group, scale_log2, out, out_dtype, os);
     else
       launch_attn<128, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                  group, scale_log2, out, out_dtype);
+                                  group, scale_log2, out, out_dtype, os);
   } else {
     if (q_dtype == SI_DT_BF16)
       launch_attn<64, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                  group, scale_log2, out, out_dtype);
+                                  group, scale_log2, out, out_dtype, os);
     else
       launch_attn<64, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                 group, scale_log2, out, out_dtype);
+                                 group, scale_log2, out, out_dtype, os);
   }
   return check_launch("si_attn_packed_fwd");
+}
+}  // namespace
+
+extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
+                                  int64_t D, const int8_t* code, const int32_t* slot,
+                                  const void* const* buckets, int scale_dtype, int64_t S_kv,
+                                  int64_t group, float sm_scale, void* out, int out_dtype,
+                                  void* workspace, size_t workspace_bytes, si_stream_t stream) {
+  clear_error();
+  const OutStrides os{H * S_q * D, S_q * D, D};
+  return run_attn(q, q_dtype, B, H, S_q, D, code, slot, buckets, scale_dtype, S_kv, group,
+                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int si_attn_packed_fwd_tokens(const void* q, int q_dtype, int64_t B, int64_t H,
+                                         int64_t S_q, int64_t D, const int8_t* code,
+                                         const int32_t* slot, const void* const* buckets,
+                                         int scale_dtype, int64_t S_kv, int64_t group,
+                                         float sm_scale, void* out, int out_dtype,
+                                         void* workspace, size_t workspace_bytes,
+                                         si_stream_t stream) {
+  clear_error();
+  const OutStrides os{S_q * H * D, D, H * D};
+  return run_attn(q, q_dtype, B, H, S_q, D, code, slot, buckets, scale_dtype, S_kv, group,
+                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, as_stream(stream));
 }

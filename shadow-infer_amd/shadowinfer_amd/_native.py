@@ -61,6 +61,8 @@ _SIGNATURES = {
     "si_attn_workspace_bytes": (_sz, [_i64, _i64]),
     "si_attn_packed_fwd": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i64,
                                   _i64, ctypes.c_float, _vp, _i32, _vp, _sz, _vp]),
+    "si_attn_packed_fwd_tokens": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
+                                         _i64, _i64, ctypes.c_float, _vp, _i32, _vp, _sz, _vp]),
     "si_quant_rows_i8": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp]),
     "si_quant_rows_i4": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_int4_pack_rows": (_i32, [_vp, _i64, _i64, _vp, _vp]),
@@ -76,6 +78,10 @@ _SIGNATURES = {
     "si_admit_workspace_bytes": (_sz, [_i64]),
     "si_admit_codes": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
                               _vp, _vp, _sz, _vp]),
+    "si_rmsnorm_rows": (_i32, [_vp, _i32, _i64, _i64, _vp, ctypes.c_float, _vp, _vp, _vp, _vp]),
+    "si_rope_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "si_swiglu_quant": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "si_row_argmax_conf": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp]),
     "si_int8_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "si_int8_linear_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                       _sz, _vp]),

@@ -20,10 +20,14 @@ from .packed_kv_cache import PackedKVCache
 
 
 def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[float] = None,
-                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                     out_dtype: torch.dtype = torch.float32,
+                     token_major: bool = False) -> torch.Tensor:
     """``q`` ``[B, H, S_q, D]`` (bf16 or fp16) against the cache's K/V
     ``[B, H, S_kv, D]``; returns ``[B, H, S_q, D]`` in ``out_dtype`` (fp32 by
-    default, the dtype of attention over the fp32 tensors unpack() returns)."""
+    default, the dtype of attention over the fp32 tensors unpack() returns).
+    ``token_major=True`` returns ``[B, S_q, H, D]`` instead, written directly
+    by the kernel: the ``attn.transpose(1, 2)`` layout an output projection
+    reads (models/diffusion_llama.py:390-391)."""
     if q.dim() != 4:
         raise ValueError(f"q must be [batch, heads, seq, dim], got {tuple(q.shape)}")
     B, H, Sq, D = q.shape
@@ -40,10 +44,12 @@ def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[f
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     qc = q.contiguous()
-    out = torch.empty(qc.shape, dtype=out_dtype, device=qc.device)
+    shape = (B, Sq, H, D) if token_major else (B, H, Sq, D)
+    out = torch.empty(shape, dtype=out_dtype, device=qc.device)
     ws_bytes = _native.size_query("si_attn_workspace_bytes", H, cache.seq_len)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=qc.device)
-    _native.call("si_attn_packed_fwd", qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
+    entry = "si_attn_packed_fwd_tokens" if token_major else "si_attn_packed_fwd"
+    _native.call(entry, qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
                  code.data_ptr(), slot.data_ptr(), table, sdt, cache.seq_len, group,
                  float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype), ws.data_ptr(),
                  ws_bytes, _native.stream(q.device))
