@@ -195,6 +195,22 @@ int si_attn_packed_fwd_tokens(const void* q, int q_dtype, int64_t B, int64_t H, 
                               int64_t group, float sm_scale, void* out, int out_dtype,
                               void* workspace, size_t workspace_bytes, si_stream_t stream);
 
+/* The per-head slot lists si_attn_packed_fwd builds on every call (tiles of
+ * one precision per head) depend only on code and slot, i.e. on the plan:
+ * build them once into lists (si_attn_workspace_bytes(H, S_kv) bytes,
+ * 16-byte aligned) and reuse them for every cache packed with that plan. */
+int si_attn_build_lists(const int8_t* code, const int32_t* slot, int64_t H, int64_t S_kv,
+                        void* lists, size_t lists_bytes, si_stream_t stream);
+
+/* si_attn_packed_fwd (token_major == 0: out [B, H, S_q, D]) or
+ * si_attn_packed_fwd_tokens (token_major != 0: out [B, S_q, H, D]) over lists
+ * built by si_attn_build_lists. */
+int si_attn_packed_fwd_built(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
+                             int64_t D, const void* lists, size_t lists_bytes,
+                             const void* const* buckets, int scale_dtype, int64_t S_kv,
+                             int64_t group, float sm_scale, void* out, int out_dtype,
+                             int token_major, si_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Quantizer                                                               */
 /* ---------------------------------------------------------------------- */

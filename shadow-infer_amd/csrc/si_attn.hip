@@ -707,7 +707,8 @@ namespace {
 int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int64_t D,
              const int8_t* code, const int32_t* slot, const void* const* buckets, int scale_dtype,
              int64_t S_kv, int64_t group, float sm_scale, void* out, int out_dtype,
-             const OutStrides& os, void* workspace, size_t workspace_bytes, hipStream_t st) {
+             const OutStrides& os, void* workspace, size_t workspace_bytes, bool build_lists,
+             hipStream_t st) {
   SI_CHECK_ARG(q_dtype == SI_DT_BF16 || q_dtype == SI_DT_F16,
                "si_attn_packed_fwd: q dtype must be bf16 or fp16 (got %d)", q_dtype);
   SI_CHECK_ARG(dtype_ok(scale_dtype), "si_attn_packed_fwd: unsupported scale dtype %d",
@@ -722,7 +723,8 @@ int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int6
   SI_CHECK_ARG(H < 65536 && B < 65536 && S_kv < ((int64_t)1 << 30),
                "si_attn_packed_fwd: H and B must be < 65536, S_kv < 2^30");
   if (B * H * S_q == 0) return SI_OK;
-  SI_CHECK_ARG(q && code && slot && buckets && out, "si_attn_packed_fwd: NULL argument");
+  SI_CHECK_ARG(q && buckets && out && (!build_lists || (code && slot)),
+               "si_attn_packed_fwd: NULL argument");
   const size_t need = si_attn_workspace_bytes(H, S_kv);
   SI_CHECK_ARG(workspace != nullptr && workspace_bytes >= need &&
                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
@@ -734,8 +736,10 @@ int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int6
   const int64_t cap = list_cap(S_kv);
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
   int32_t* lists = counts + H * 8;
-  attn_lists<<<(unsigned)H, 256, 0, st>>>(code, slot, H, S_kv, cap, counts, lists);
-  if (int rc = check_launch("si_attn_packed_fwd")) return rc;
+  if (build_lists) {
+    attn_lists<<<(unsigned)H, 256, 0, st>>>(code, slot, H, S_kv, cap, counts, lists);
+    if (int rc = check_launch("si_attn_packed_fwd")) return rc;
+  }
   const int64_t bmq = D == 128 ? AttnCfg<128>::BMQ : AttnCfg<64>::BMQ;
   const dim3 grid((unsigned)ceil_div(S_q, bmq), (unsigned)H, (unsigned)B);
   const float scale_log2 = sm_scale * 1.4426950408889634f;
@@ -767,7 +771,8 @@ extern "C" int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t
   clear_error();
   const OutStrides os{H * S_q * D, S_q * D, D};
   return run_attn(q, q_dtype, B, H, S_q, D, code, slot, buckets, scale_dtype, S_kv, group,
-                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, as_stream(stream));
+                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, true,
+                  as_stream(stream));
 }
 
 extern "C" int si_attn_packed_fwd_tokens(const void* q, int q_dtype, int64_t B, int64_t H,
@@ -780,5 +785,39 @@ extern "C" int si_attn_packed_fwd_tokens(const void* q, int q_dtype, int64_t B, 
   clear_error();
   const OutStrides os{S_q * H * D, D, H * D};
   return run_attn(q, q_dtype, B, H, S_q, D, code, slot, buckets, scale_dtype, S_kv, group,
-                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, as_stream(stream));
+                  sm_scale, out, out_dtype, os, workspace, workspace_bytes, true,
+                  as_stream(stream));
+}
+
+extern "C" int si_attn_build_lists(const int8_t* code, const int32_t* slot, int64_t H,
+                                   int64_t S_kv, void* workspace, size_t workspace_bytes,
+                                   si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(H >= 0 && H < 65536 && S_kv > 0 && S_kv < ((int64_t)1 << 30),
+               "si_attn_build_lists: bad shape");
+  if (H == 0) return SI_OK;
+  SI_CHECK_ARG(code && slot, "si_attn_build_lists: NULL argument");
+  const size_t need = si_attn_workspace_bytes(H, S_kv);
+  SI_CHECK_ARG(workspace != nullptr && workspace_bytes >= need &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+               "si_attn_build_lists: workspace too small or misaligned (%zu < %zu bytes)",
+               workspace_bytes, need);
+  int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+  attn_lists<<<(unsigned)H, 256, 0, as_stream(stream)>>>(code, slot, H, S_kv, list_cap(S_kv),
+                                                          counts, counts + H * 8);
+  return check_launch("si_attn_build_lists");
+}
+
+extern "C" int si_attn_packed_fwd_built(const void* q, int q_dtype, int64_t B, int64_t H,
+                                        int64_t S_q, int64_t D, const void* lists,
+                                        size_t lists_bytes, const void* const* buckets,
+                                        int scale_dtype, int64_t S_kv, int64_t group,
+                                        float sm_scale, void* out, int out_dtype,
+                                        int token_major, si_stream_t stream) {
+  clear_error();
+  const OutStrides os = token_major ? OutStrides{S_q * H * D, D, H * D}
+                                    : OutStrides{H * S_q * D, S_q * D, D};
+  return run_attn(q, q_dtype, B, H, S_q, D, nullptr, nullptr, buckets, scale_dtype, S_kv, group,
+                  sm_scale, out, out_dtype, os, const_cast<void*>(lists), lists_bytes, false,
+                  as_stream(stream));
 }

@@ -833,7 +833,23 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (M <= 640 && K % 128 == 0) {
     kind = K_DMA_256x128_K128;  // M = 512: 37 us
   } else if (K % 128 == 0) {
-    kind = K_DMA8_256x192_K128;  // M = 1024: 61 us, M = 2048: 125 us
+    // Large M: one tile per CU per wave of tiles, so the tile count decides
+    // how full the last wave is. Score = (tiles / tiles rounded up to whole
+    // waves of 256 CUs) x the tile's own speed relative to 256x256 (measured
+    // on equally filled grids: 1 : 0.91 : 0.81). 1024x11008x4096 -> 256x192,
+    // 2048x22016x4096 -> 256x256, 2048x4096x11008 -> 256x128.
+    struct Cand { int kind, bm, bn; double speed; };
+    const Cand cands[3] = {{K_DMA8_256x192_K128, 256, 192, 0.91},
+                           {K_DMA8_256x256, 256, 256, 1.0},
+                           {K_DMA_256x128_K128, 256, 128, 0.81}};
+    double best = -1.0;
+    kind = K_DMA8_256x192_K128;
+    for (const Cand& c : cands) {
+      const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+      const double fill = (double)tiles / (double)(ceil_div(tiles, 256) * 256);
+      const double score = fill * c.speed;
+      if (score > best + 1e-9) { best = score; kind = c.kind; }
+    }
   } else if (K % 64 == 0) {
     kind = K_DMA_256x192;
   } else {

@@ -255,7 +255,9 @@ __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu,
 // Per-position argmax and confidence (schedule_round, block_decoding.py:148-151):
 // tok[m] = the first index of the largest logit (a NaN counts as largest),
 // conf[m] = max softmax probability = 1 / sum_v exp(l_v - l_max), in fp32.
-// One block per row, two passes (the second from L2).
+// One block per row, one pass: each thread keeps its best (value, index) and
+// the sum of exp(l - its running max), rescaled when the max grows; partial
+// results merge by the same rule. 16-byte loads when rows allow.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool beats(float a, int64_t ia, float b, int64_t ib) {
   const bool na = a != a, nb = b != b;
@@ -263,41 +265,67 @@ __device__ __forceinline__ bool beats(float a, int64_t ia, float b, int64_t ib) 
   return a > b || (a == b && ia < ib);
 }
 
-__global__ __launch_bounds__(256) void row_argmax_conf(const void* __restrict__ logits, int dt,
+struct ArgSum {
+  float m;     // running max (NaN once a NaN was seen)
+  int64_t i;   // its first index
+  float s;     // sum of exp(l - m)
+};
+
+__device__ __forceinline__ void arg_add(ArgSum& a, float x, int64_t i) {
+  if (beats(x, i, a.m, a.i)) {
+    if (x != a.m) a.s = a.m == -INFINITY ? 0.0f : a.s * expf(a.m - x);
+    a.m = x;
+    a.i = i;
+  }
+  a.s += x == -INFINITY ? 0.0f : expf(x - a.m);
+}
+
+__device__ __forceinline__ void arg_merge(ArgSum& a, const ArgSum& b) {
+  const float m = beats(b.m, b.i, a.m, a.i) ? b.m : a.m;
+  const float sa = a.m == -INFINITY ? 0.0f : a.s * expf(a.m - m);
+  const float sb = b.m == -INFINITY ? 0.0f : b.s * expf(b.m - m);
+  if (beats(b.m, b.i, a.m, a.i)) a.i = b.i;
+  a.m = m;
+  a.s = sa + sb;
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void row_argmax_conf(const void* __restrict__ logits,
                                                        int64_t M, int64_t V,
                                                        int64_t* __restrict__ tok,
                                                        float* __restrict__ conf) {
-  __shared__ float lv[4];
+  __shared__ float lm[4], ls[4];
   __shared__ int64_t li[4];
-  __shared__ float lds[4];
   for (int64_t m = blockIdx.x; m < M; m += gridDim.x) {
-    float best = -INFINITY;
-    int64_t bi = INT64_MAX;
-    for (int64_t v = threadIdx.x; v < V; v += blockDim.x) {
-      const float x = load_any(logits, dt, m * V + v);
-      if (beats(x, v, best, bi)) { best = x; bi = v; }
+    ArgSum a{-INFINITY, INT64_MAX, 0.0f};
+    if constexpr (VEC) {
+      for (int64_t c = threadIdx.x; c < V / 8; c += blockDim.x) {
+        float v[8];
+        load8<DT>(logits, m * V + c * 8, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) arg_add(a, v[e], c * 8 + e);
+      }
+    } else {
+      for (int64_t v = threadIdx.x; v < V; v += blockDim.x) arg_add(a, load_any(logits, DT, m * V + v), v);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off, 64);
-      const int64_t oi = __shfl_xor(bi, off, 64);
-      if (beats(ob, oi, best, bi)) { best = ob; bi = oi; }
+      ArgSum b{__shfl_xor(a.m, off, 64), __shfl_xor(a.i, off, 64), __shfl_xor(a.s, off, 64)};
+      arg_merge(a, b);
     }
-    if ((threadIdx.x & 63) == 0) { lv[threadIdx.x >> 6] = best; li[threadIdx.x >> 6] = bi; }
+    if ((threadIdx.x & 63) == 0) {
+      lm[threadIdx.x >> 6] = a.m;
+      li[threadIdx.x >> 6] = a.i;
+      ls[threadIdx.x >> 6] = a.s;
+    }
     __syncthreads();
-    best = lv[0];
-    bi = li[0];
-    for (int w = 1; w < 4; ++w)
-      if (beats(lv[w], li[w], best, bi)) { best = lv[w]; bi = li[w]; }
-    __syncthreads();
-    float sum = 0.0f;
-    for (int64_t v = threadIdx.x; v < V; v += blockDim.x)
-      sum += expf(load_any(logits, dt, m * V + v) - best);
-    sum = block_sum(sum, lds);
     if (threadIdx.x == 0) {
-      tok[m] = bi == INT64_MAX ? 0 : bi;
-      conf[m] = 1.0f / sum;
+      ArgSum r{lm[0], li[0], ls[0]};
+      for (int w = 1; w < 4; ++w) arg_merge(r, ArgSum{lm[w], li[w], ls[w]});
+      tok[m] = r.i == INT64_MAX ? 0 : r.i;
+      conf[m] = 1.0f / r.s;
     }
+    __syncthreads();
   }
 }
 
@@ -405,7 +433,18 @@ extern "C" int si_row_argmax_conf(const void* logits, int dtype, int64_t M, int6
   SI_CHECK_ARG(M >= 0 && V > 0, "si_row_argmax_conf: bad shape");
   if (M == 0) return SI_OK;
   SI_CHECK_ARG(logits && tokens && confidence, "si_row_argmax_conf: NULL argument");
-  row_argmax_conf<<<row_grid(M), 256, 0, as_stream(stream)>>>(logits, dtype, M, V, tokens,
-                                                              confidence);
+  hipStream_t st = as_stream(stream);
+  const unsigned g = row_grid(M);
+  const bool vec = V % 8 == 0 && aligned16(logits);
+  if (dtype == SI_DT_BF16) {
+    if (vec) row_argmax_conf<SI_DT_BF16, true><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+    else row_argmax_conf<SI_DT_BF16, false><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+  } else if (dtype == SI_DT_F16) {
+    if (vec) row_argmax_conf<SI_DT_F16, true><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+    else row_argmax_conf<SI_DT_F16, false><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+  } else {
+    if (vec) row_argmax_conf<SI_DT_F32, true><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+    else row_argmax_conf<SI_DT_F32, false><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
+  }
   return check_launch("si_row_argmax_conf");
 }

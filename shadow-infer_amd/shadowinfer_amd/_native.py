@@ -63,6 +63,9 @@ _SIGNATURES = {
                                   _i64, ctypes.c_float, _vp, _i32, _vp, _sz, _vp]),
     "si_attn_packed_fwd_tokens": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
                                          _i64, _i64, ctypes.c_float, _vp, _i32, _vp, _sz, _vp]),
+    "si_attn_build_lists": (_i32, [_vp, _vp, _i64, _i64, _vp, _sz, _vp]),
+    "si_attn_packed_fwd_built": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _sz, _vp, _i32,
+                                        _i64, _i64, ctypes.c_float, _vp, _i32, _i32, _vp]),
     "si_quant_rows_i8": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp]),
     "si_quant_rows_i4": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_int4_pack_rows": (_i32, [_vp, _i64, _i64, _vp, _vp]),

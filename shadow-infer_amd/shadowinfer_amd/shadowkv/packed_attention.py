@@ -38,7 +38,7 @@ def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[f
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"q must be bfloat16 or float16, got {q.dtype}")
     _native.require_device(q, "packed_attention")
-    code, slot, table, sdt, group = cache.device_state()
+    code, _, table, sdt, group = cache.device_state()
     if code.device != q.device:
         raise ValueError("q and the packed cache live on different devices")
     if sm_scale is None:
@@ -46,11 +46,9 @@ def packed_attention(q: torch.Tensor, cache: PackedKVCache, sm_scale: Optional[f
     qc = q.contiguous()
     shape = (B, Sq, H, D) if token_major else (B, H, Sq, D)
     out = torch.empty(shape, dtype=out_dtype, device=qc.device)
-    ws_bytes = _native.size_query("si_attn_workspace_bytes", H, cache.seq_len)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=qc.device)
-    entry = "si_attn_packed_fwd_tokens" if token_major else "si_attn_packed_fwd"
-    _native.call(entry, qc.data_ptr(), _native.dtype_code(q.dtype), B, H, Sq, D,
-                 code.data_ptr(), slot.data_ptr(), table, sdt, cache.seq_len, group,
-                 float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype), ws.data_ptr(),
-                 ws_bytes, _native.stream(q.device))
+    lists = cache.attention_lists()
+    _native.call("si_attn_packed_fwd_built", qc.data_ptr(), _native.dtype_code(q.dtype), B, H,
+                 Sq, D, lists.data_ptr(), lists.numel(), table, sdt, cache.seq_len, group,
+                 float(sm_scale), out.data_ptr(), _native.dtype_code(out_dtype),
+                 1 if token_major else 0, _native.stream(q.device))
     return out

@@ -444,6 +444,13 @@ class PackedKVCache:
         return (self._grouping.code, self._grouping.slot, self._bucket_table(),
                 _native.dtype_code(self._scale_dtype), self._group_size)
 
+    def attention_lists(self) -> torch.Tensor:
+        """The fused attention's per-head slot lists for this cache's grouping
+        (built once per plan and shared by every cache packed with it)."""
+        if self._grouping is None:
+            raise ValueError("cache holds no packed data")
+        return self._grouping.attn_lists(self.seq_len, self.num_heads)
+
     def __repr__(self) -> str:
         return (f"PackedKVCache(batch={self.batch_size}, heads={self.num_heads}, "
                 f"seq_len={self.seq_len}, head_dim={self.head_dim}, "

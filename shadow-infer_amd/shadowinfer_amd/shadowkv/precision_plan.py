@@ -71,10 +71,13 @@ class DeviceGrouping:
     ``slot``: int32 [S*H] bucket positions (-1 if absent);
     ``counts``: entries per code 0..4 (host ints);
     ``flat``: per precision, int64 ``h*S + t`` of the bucket's entries in
-    slot order (the plan's ``flat_indices``), built on first use.
+    slot order (the plan's ``flat_indices``), built on first use;
+    ``attn``: the fused attention's per-head slot lists, built on first use.
+    The tensors are never modified in place (eviction makes a new grouping),
+    so what is derived from them stays valid.
     """
 
-    __slots__ = ("code", "slot", "counts", "flat")
+    __slots__ = ("code", "slot", "counts", "flat", "attn")
 
     def __init__(self, code: torch.Tensor, slot: torch.Tensor, counts: List[int],
                  flat: Optional[List[torch.Tensor]] = None):
@@ -82,6 +85,18 @@ class DeviceGrouping:
         self.slot = slot
         self.counts = counts
         self.flat = flat
+        self.attn: Optional[torch.Tensor] = None
+
+    def attn_lists(self, S: int, H: int) -> torch.Tensor:
+        """Per-head slot lists of the fused attention (si_attn_build_lists)."""
+        if self.attn is None:
+            dev = self.code.device
+            n = _native.size_query("si_attn_workspace_bytes", H, S)
+            lists = torch.empty(max(n, 16), dtype=torch.uint8, device=dev)
+            _native.call("si_attn_build_lists", self.code.data_ptr(), self.slot.data_ptr(), H, S,
+                         lists.data_ptr(), n, _native.stream(dev))
+            self.attn = lists
+        return self.attn
 
     def flat_lists(self, S: int, H: int) -> List[torch.Tensor]:
         """Per-precision ``h*S + t`` lists in slot order (si_plan_scatter)."""

@@ -113,3 +113,33 @@ def test_attention_errors(dev):
         packed_attention(torch.randn(1, 3, 8, 64, device=dev, dtype=torch.bfloat16), cache)
     with pytest.raises(TypeError):
         packed_attention(torch.randn(1, 2, 8, 64, device=dev), cache)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_entry_points_agree(dev, D):
+    """si_attn_packed_fwd / _tokens (slot lists built on every call) and
+    si_attn_packed_fwd_built (lists built once per plan) give the same bits,
+    and a cache repacked with the same plan reuses the plan's lists."""
+    from shadowinfer_amd import _native
+    B, H, S = 2, 3, 200
+    k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=D)
+    q, _ = kv_inputs(B, H, S, D, torch.bfloat16, seed=D + 1)
+    codes = mixed_codes(S, H, seed=D, probs=(1, 1, 1, 1), evicted=0.1)
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    cache = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    qd = q.to(dev)
+    code, slot, table, sdt, group = cache.device_state()
+    ws_bytes = _native.size_query("si_attn_workspace_bytes", H, S)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    for entry, tm in (("si_attn_packed_fwd", False), ("si_attn_packed_fwd_tokens", True)):
+        shape = (B, S, H, D) if tm else (B, H, S, D)
+        out = torch.empty(shape, dtype=torch.float32, device=dev)
+        _native.call(entry, qd.data_ptr(), _native.dtype_code(qd.dtype), B, H, S, D,
+                     code.data_ptr(), slot.data_ptr(), table, sdt, S, group,
+                     float(1 / D ** 0.5), out.data_ptr(), _native.dtype_code(torch.float32),
+                     ws.data_ptr(), ws_bytes, _native.stream(dev))
+        got = packed_attention(qd, cache, token_major=tm)
+        assert torch.equal(got, out)
+    again = PackedKVCache.pack((k * 2).to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    assert again.attention_lists() is cache.attention_lists()

@@ -61,12 +61,14 @@ def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
     np.testing.assert_array_equal(c, O.gemm_i8(a.numpy(), b.numpy()))
 
 
-@pytest.mark.parametrize("M", [256, 1024])
-def test_gemm_i32_large_m_exact(dev, M):
-    """Full FFN shape at large M against the exact float64 product."""
-    g = torch.Generator().manual_seed(M)
-    a = torch.randint(-127, 128, (M, 4096), generator=g, dtype=torch.int8).to(dev)
-    b = torch.randint(-127, 128, (4096, 11008), generator=g, dtype=torch.int8).to(dev)
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 11008), (1024, 4096, 11008),
+                                   (2048, 4096, 22016), (2048, 11008, 4096)])
+def test_gemm_i32_large_m_exact(dev, M, K, N):
+    """FFN shapes at large M (up, fused gate|up and down of a 2048-token step,
+    each on its own tile shape) against the exact float64 product."""
+    g = torch.Generator().manual_seed(M + K)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    b = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(dev)
     c = _gemm_i32(a, b)
     assert torch.equal(c.to(torch.int64), _exact_i32(a, b))
 
