@@ -819,6 +819,15 @@ int forced_kind() {
   return kind;
 }
 
+// Split-K override for tuning sweeps of the tile kernels: SI_GEMM_SPLITS=<n>.
+int forced_splits() {
+  static const int splits = [] {
+    const char* v = getenv("SI_GEMM_SPLITS");
+    return v != nullptr ? atoi(v) : 0;
+  }();
+  return splits;
+}
+
 Plan choose(int64_t M, int64_t N, int64_t K) {
   Plan p{K_SCALAR, 0, 1, (int)K, 0, 0, 0};
   const bool big = M >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 31);
@@ -829,7 +838,7 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (M <= 32 && K % 64 == 0) {
     kind = K_STREAM_N64;  // 4096 x 11008: M = 1 13 us, M = 16 14 us, M = 32 16 us
   } else if (M <= 384 && K % 128 == 0) {
-    kind = K_DMA_128x128;  // M = 64: 21 us, M = 256: 25 us
+    kind = K_DMA_128x128;  // M = 64: 17.5 us (2 K splits), M = 256: 25 us
   } else if (M <= 640 && K % 128 == 0) {
     kind = K_DMA_256x128_K128;  // M = 512: 37 us
   } else if (K % 128 == 0) {
@@ -906,6 +915,20 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   }
   p.splits = 1;
   p.k_split = (int)K;
+  int want = forced_splits();
+  if (want <= 0 && forced_kind() < 0 && p.kind == K_DMA_128x128 &&
+      ceil_div(M, 128) * ceil_div(N, 128) <= 128 && K / p.bk >= 16) {
+    // At most half the CUs would hold a tile: two K halves (int32 partials
+    // summed by gemm_finalize) use all of them. 33..64 x 11008 x 4096:
+    // 20-21 us -> 15-17.5 us; with 172 tiles (N = 22016) splitting is slower.
+    want = 2;
+  }
+  if (want > 1 && p.kind != K_TILE_128x128) {
+    const int64_t kt = K / p.bk;
+    const int64_t per = ceil_div(kt, want);
+    p.k_split = (int)(per * p.bk);
+    p.splits = (int)ceil_div(kt, per);
+  }
   return p;
 }
 
