@@ -799,7 +799,9 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             // eight waves per block (two per SIMD)
             K_DMA8_256x256 = 13, K_DMA8_256x256_K128 = 14, K_DMA8_256x192_K128 = 15,
             K_DMA8_256x128 = 16, K_DMA8_128x256 = 17,
-            K_STREAM_N64 = 25, K_STREAM_N64_W8 = 27 };
+            K_STREAM_N64 = 25, K_STREAM_N64_W8 = 27,
+            // eight waves on a 128x128 tile (4x2 and 2x4 wave grids)
+            K_DMA8_128x128_42 = 30, K_DMA8_128x128_24 = 31 };
 
 struct Plan {
   int kind;
@@ -837,27 +839,23 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     kind = forced_kind();
   } else if (M <= 32 && K % 64 == 0) {
     kind = K_STREAM_N64;  // 4096 x 11008: M = 1 13 us, M = 16 14 us, M = 32 16 us
-  } else if (M <= 384 && K % 128 == 0) {
-    kind = K_DMA_128x128;  // M = 64: 17.5 us (2 K splits), M = 256: 25 us
-  } else if (M <= 640 && K % 128 == 0) {
-    kind = K_DMA_256x128_K128;  // M = 512: 37 us
   } else if (K % 128 == 0) {
-    // Large M: one tile per CU per wave of tiles, so the tile count decides
-    // how full the last wave is. Score = (tiles / tiles rounded up to whole
-    // waves of 256 CUs) x the tile's own speed relative to 256x256 (measured
-    // on equally filled grids: 1 : 0.91 : 0.81). 1024x11008x4096 -> 256x192,
-    // 2048x22016x4096 -> 256x256, 2048x4096x11008 -> 256x128.
+    // One tile per CU per wave of tiles. Estimated time = waves of 256 tiles
+    // x (tile area / the tile's measured speed relative to 256x256); the
+    // smallest wins. 4096 x 11008: M = 64..256 -> 128x128 (M = 256: 21.7 us),
+    // M = 384..512 -> 256x128, M = 640 -> 128x128, M = 1024 -> 256x192;
+    // 2048 x 22016 x 4096 -> 256x256; 2048 x 4096 x 11008 -> 256x128.
     struct Cand { int kind, bm, bn; double speed; };
-    const Cand cands[3] = {{K_DMA8_256x192_K128, 256, 192, 0.91},
+    const Cand cands[4] = {{K_DMA8_256x192_K128, 256, 192, 0.91},
                            {K_DMA8_256x256, 256, 256, 1.0},
-                           {K_DMA_256x128_K128, 256, 128, 0.81}};
-    double best = -1.0;
+                           {K_DMA_256x128_K128, 256, 128, 0.81},
+                           {K_DMA8_128x128_24, 128, 128, 0.78}};
+    double best = 0.0;
     kind = K_DMA8_256x192_K128;
     for (const Cand& c : cands) {
       const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn);
-      const double fill = (double)tiles / (double)(ceil_div(tiles, 256) * 256);
-      const double score = fill * c.speed;
-      if (score > best + 1e-9) { best = score; kind = c.kind; }
+      const double t = (double)ceil_div(tiles, 256) * c.bm * c.bn / c.speed;
+      if (best == 0.0 || t < best * (1.0 - 1e-9)) { best = t; kind = c.kind; }
     }
   } else if (K % 64 == 0) {
     kind = K_DMA_256x192;
@@ -902,6 +900,8 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     case K_DMA8_256x192_K128: p.bm = 256; p.bn = 192; p.bk = 128; break;
     case K_DMA8_256x128: p.bm = 256; p.bn = 128; p.bk = 64; break;
     case K_DMA8_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
+    case K_DMA8_128x128_42: p.bm = 128; p.bn = 128; p.bk = 128; break;
+    case K_DMA8_128x128_24: p.bm = 128; p.bn = 128; p.bk = 128; break;
     default: p.kind = K_TILE_128x128; p.bm = 128; p.bn = 128; p.bk = 128; break;
   }
   if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0 && p.kind != K_TILE_128x128) {
@@ -916,11 +916,13 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   p.splits = 1;
   p.k_split = (int)K;
   int want = forced_splits();
-  if (want <= 0 && forced_kind() < 0 && p.kind == K_DMA_128x128 &&
+  if (want <= 0 && forced_kind() < 0 && M <= 64 &&
+      (p.kind == K_DMA_128x128 || p.kind == K_DMA8_128x128_24) &&
       ceil_div(M, 128) * ceil_div(N, 128) <= 128 && K / p.bk >= 16) {
     // At most half the CUs would hold a tile: two K halves (int32 partials
     // summed by gemm_finalize) use all of them. 33..64 x 11008 x 4096:
-    // 20-21 us -> 15-17.5 us; with 172 tiles (N = 22016) splitting is slower.
+    // 20-21 us -> 15-17.5 us. Not with 172 tiles (N = 22016), and not from
+    // M = 128 on, where the partial traffic outweighs the gain.
     want = 2;
   }
   if (want > 1 && p.kind != K_TILE_128x128) {
@@ -965,6 +967,8 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
     case K_DMA8_256x256_K128: SI_DMA(256, 256, 128, 4, 2, 2); break;
     case K_DMA8_256x192_K128: SI_DMA(256, 192, 128, 4, 2, 2); break;
     case K_DMA8_256x128: SI_DMA(256, 128, 64, 4, 2, 4); break;
+    case K_DMA8_128x128_42: SI_DMA(128, 128, 128, 4, 2, 4); break;
+    case K_DMA8_128x128_24: SI_DMA(128, 128, 128, 2, 4, 4); break;
     default: SI_DMA(128, 256, 64, 2, 4, 4); break;
   }
 #undef SI_DMA
