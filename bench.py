@@ -218,12 +218,77 @@ def bench_kv(torch, dev, steps, warmup):
     res["compress_gbs"] = c_bytes / (ms_c * 1e-3) / 1e9
     res["compress_bytes"] = c_bytes
 
-    # Reuse (50% mask) and evict (25%) on one layer, for context.
-    prev = layers[1]["cache"]
-    cur = layers[0]["cache"]
-    mask = (torch.rand(S, H, generator=gen, device=dev) < 0.5)
-    ms_reuse = timer.time(lambda: cur.apply_reuse_mask(prev, mask), 5)
+    # apply_reuse_mask (50% of the token-heads, previous step's cache packed
+    # with the same plan) and evict (25%) on one layer, timed at the ABI like
+    # pack/unpack. Algorithmic bytes: every reused entry is read from the
+    # previous buckets and written into the current ones; evict reads and
+    # writes every surviving entry of the buckets it rebuilds.
+    L0 = layers[0]
+    k2, v2 = make_kv(gen, dev, torch.bfloat16)
+    prev = PackedKVCache.pack(k2, v2, None, group_size=GROUP, plan=L0["plan"])["packed_kv"]
+    pcode, pslot, ptable, _, _ = prev.device_state()
+    cur = L0["cache"]
+    entry_b = torch.tensor([2 * B * D * 4, 2 * B * D * 2, 2 * B * (D + 2), 2 * B * (D // 2 + 2 * (D // GROUP)), 0],
+                           dtype=torch.int64, device=dev)  # K + V bytes of one token-head per code
+    code_l = L0["code"].to(torch.int64)
+    reuse_m = (torch.rand(S * H, generator=gen, device=dev) < 0.5)
+    reuse_u8m = reuse_m.to(torch.uint8)
+
+    def reuse():
+        _native.call("si_kv_reuse_flat", L0["flat"], L0["counts"], L0["table"], S, pcode.data_ptr(),
+                     pslot.data_ptr(), ptable, S, reuse_u8m.data_ptr(), H, B, D, GROUP, L0["sdt"],
+                     None, sptr)
+
+    reuse()
+    ms_reuse = timer.time(reuse, 20)
+    r_bytes = int((entry_b[code_l] * reuse_m).sum()) * 2 + S * H * 11  # + codes, slots, mask
     res["reuse50_us"] = ms_reuse * 1e3
+    res["reuse50_bytes"] = r_bytes
+    res["reuse50_gbs"] = r_bytes / (ms_reuse * 1e-3) / 1e9
+    t0 = time.perf_counter()
+    for _ in range(5):
+        cur.apply_reuse_mask(prev, reuse_m.view(S, H))
+    torch.cuda.synchronize()
+    res["reuse50_api_us"] = (time.perf_counter() - t0) / 5 * 1e6
+
+    ev_m = (torch.rand(S * H, generator=gen, device=dev) < 0.25)
+    ev_u8 = ev_m.to(torch.uint8)
+    ws_b = _native.size_query("si_plan_workspace_bytes", S * H)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device=dev)
+    n_code = torch.empty(S * H, dtype=torch.int8, device=dev)
+    n_slot = torch.empty(S * H, dtype=torch.int32, device=dev)
+    n_cnt = torch.empty(5, dtype=torch.int64, device=dev)
+    _native.call("si_plan_scan", L0["code"].data_ptr(), ev_u8.data_ptr(), S * H, n_code.data_ptr(),
+                 n_slot.data_ptr(), n_cnt.data_ptr(), ws.data_ptr(), ws_b, sptr)
+    new_counts = [int(c) for c in n_cnt.tolist()]
+    fresh = cur._alloc_buckets(new_counts, dev, torch.bfloat16)
+    ftable = cur._bucket_table(fresh)
+    n_flat = [torch.empty(new_counts[p], dtype=torch.long, device=dev) for p in range(4)]
+    n_flat_t = _native.table4([f.data_ptr() for f in n_flat])
+    n_counts = (ctypes.c_int64 * 5)(*new_counts)
+    none4 = _native.table4([None] * 4)
+
+    def evict():  # the device work of PackedKVCache.evict: rescan, new lists, compaction
+        _native.call("si_plan_scan", L0["code"].data_ptr(), ev_u8.data_ptr(), S * H,
+                     n_code.data_ptr(), n_slot.data_ptr(), n_cnt.data_ptr(), ws.data_ptr(), ws_b, sptr)
+        _native.call("si_plan_scatter", n_code.data_ptr(), n_slot.data_ptr(), S, H, n_flat_t,
+                     none4, sptr)
+        _native.call("si_kv_compact_flat", L0["slot"].data_ptr(), L0["table"], n_flat_t, n_counts,
+                     ftable, S, H, B, D, GROUP, L0["sdt"], sptr)
+
+    evict()
+    ms_ev = timer.time(evict, 20)
+    kept = ~ev_m & (code_l < 4)
+    e_bytes = int((entry_b[code_l] * kept).sum()) * 2 + S * H * 16  # + codes, slots, mask
+    res["evict25_us"] = ms_ev * 1e3
+    res["evict25_bytes"] = e_bytes
+    res["evict25_gbs"] = e_bytes / (ms_ev * 1e-3) / 1e9
+    victim = PackedKVCache.pack(k2, v2, None, group_size=GROUP, plan=L0["plan"])["packed_kv"]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    victim.evict(ev_m.view(S, H))
+    torch.cuda.synchronize()
+    res["evict25_api_us"] = (time.perf_counter() - t0) * 1e6
     del layers
     torch.cuda.empty_cache()
     return res

@@ -169,6 +169,26 @@ int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
                   const int32_t* new_slot, void* const* new_buckets, int64_t n_entries,
                   int64_t B, int64_t D, int64_t group, int scale_dtype, si_stream_t stream);
 
+/* si_kv_reuse in bucket order: walks the current cache's per-precision lists
+ * cur_flat[p] (h*S + t in slot order, cur_counts HOST int64[5] entries each;
+ * the plan's flat_indices, shadowinfer/shadowkv/precision_plan.py:144-151), one
+ * precision per block, so destination rows are contiguous. Same copies and
+ * stats as si_kv_reuse. */
+int si_kv_reuse_flat(const int64_t* const* cur_flat, const int64_t* cur_counts,
+                     void* const* cur_buckets, int64_t S, const int8_t* prev_code,
+                     const int32_t* prev_slot, const void* const* prev_buckets, int64_t S_prev,
+                     const uint8_t* mask, int64_t H, int64_t B, int64_t D, int64_t group,
+                     int scale_dtype, int64_t* stats, si_stream_t stream);
+
+/* si_kv_compact in bucket order: walks the new plan's per-precision lists
+ * new_flat[p] (new_counts HOST int64[5]); each destination row is copied from
+ * old bucket row old_slot[t*H + h]. Precisions whose new bucket pointer is NULL
+ * are left alone (their bucket is kept as it is). */
+int si_kv_compact_flat(const int32_t* old_slot, const void* const* old_buckets,
+                       const int64_t* const* new_flat, const int64_t* new_counts,
+                       void* const* new_buckets, int64_t S, int64_t H, int64_t B, int64_t D,
+                       int64_t group, int scale_dtype, si_stream_t stream);
+
 /* Bytes of device workspace si_attn_packed_fwd needs (per-head slot lists). */
 size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv);
 

@@ -12,6 +12,8 @@
 // butterfly shuffles inside the LPR lanes, so int8 (per row) and int4 (per
 // group) quantize with the same instruction stream; only the final stores
 // differ by precision. Reads walk K/V in memory order and are coalesced.
+#include <type_traits>
+
 #include "si_kv_common.h"
 
 namespace si {
@@ -1151,6 +1153,123 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Bucket-order entry copies for reuse and compaction. Each block owns kListRows
+// consecutive destination slots of one precision (the destination plan's
+// per-precision h*S + t lists, in slot order), resolves every row's source
+// slot once into LDS, then copies the K and V rows and their scales with
+// consecutive threads on consecutive units of the rows: contiguous destination
+// rows, no divergence between precisions.
+// ---------------------------------------------------------------------------
+
+constexpr int kListRows = 64;
+
+struct CopyLists {
+  const int64_t* flat[4];  // destination slot order: h*S + t
+  int64_t n[4];
+  int64_t blk_end[4];
+};
+
+template <int U>
+__device__ __forceinline__ void copy_units(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                           int64_t row_bytes, int64_t s0, int rows,
+                                           const int64_t* srcs) {
+  typedef typename std::conditional<U == 16, uint4,
+          typename std::conditional<U == 4, uint32_t,
+          typename std::conditional<U == 2, uint16_t, uint8_t>::type>::type>::type T;
+  const int64_t cpr = row_bytes / U;
+  const int64_t total = rows * cpr;
+  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
+    const int64_t r = i / cpr;
+    const int64_t c = i - r * cpr;
+    const int64_t ss = srcs[r];
+    if (ss < 0) continue;
+    *reinterpret_cast<T*>(dst + (s0 + r) * row_bytes + c * U) =
+        *reinterpret_cast<const T*>(src + ss * row_bytes + c * U);
+  }
+}
+
+// Rows s0 .. s0+rows-1 of dst <- rows srcs[r] of src (skipped where srcs[r] < 0).
+__device__ __forceinline__ void copy_rows(void* dst, const void* src, int64_t row_bytes, int64_t s0,
+                                          int rows, const int64_t* srcs) {
+  if (dst == nullptr || src == nullptr || row_bytes == 0) return;
+  uint8_t* d = reinterpret_cast<uint8_t*>(dst);
+  const uint8_t* sp = reinterpret_cast<const uint8_t*>(src);
+  const uintptr_t mis = reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(sp) |
+                        (uintptr_t)row_bytes;
+  if ((mis & 15) == 0) copy_units<16>(d, sp, row_bytes, s0, rows, srcs);
+  else if ((mis & 3) == 0) copy_units<4>(d, sp, row_bytes, s0, rows, srcs);
+  else if ((mis & 1) == 0) copy_units<2>(d, sp, row_bytes, s0, rows, srcs);
+  else copy_units<1>(d, sp, row_bytes, s0, rows, srcs);
+}
+
+// REUSE: destination = current cache, source = previous cache (same H, so the
+// same token-major entry id); a row is copied when mask[e] is set, t < S_src
+// and the previous code equals the row's precision (apply_reuse_mask,
+// packed_kv_cache.py:791-852). Otherwise (compaction, :698-737): every row is
+// copied from src_slot[e] of the old buckets.
+template <bool REUSE>
+__global__ __launch_bounds__(256) void kv_copy_lists(CopyLists L, Buckets dst, Buckets src,
+                                                     const int8_t* __restrict__ src_code,
+                                                     const int32_t* __restrict__ src_slot,
+                                                     const uint8_t* __restrict__ mask, int64_t S,
+                                                     int64_t H, int64_t S_src, RowGeom geo,
+                                                     unsigned long long* __restrict__ stats) {
+  __shared__ int64_t srcs[kListRows];
+  __shared__ unsigned cnt[2];
+  const int64_t blk = blockIdx.x;
+  int p = 0;
+  while (p < 3 && blk >= L.blk_end[p]) ++p;
+  const int64_t s0 = (blk - (p > 0 ? L.blk_end[p - 1] : 0)) * kListRows;
+  const int rows = (int)min<int64_t>(kListRows, L.n[p] - s0);
+  if (threadIdx.x < 2) cnt[threadIdx.x] = 0u;
+  __syncthreads();
+  if ((int)threadIdx.x < rows) {
+    const int64_t f = L.flat[p][s0 + threadIdx.x];
+    const int64_t t = f % S;
+    const int64_t e = t * H + f / S;
+    int64_t ss = -1;
+    if constexpr (REUSE) {
+      if (mask[e] != 0 && t < S_src) {
+        const int pc = src_code[e];
+        if (pc == p) {
+          ss = src_slot[e];
+          atomicAdd(&cnt[0], 1u);
+        } else if (pc >= 0 && pc <= 3) {
+          atomicAdd(&cnt[1], 1u);
+        }
+      }
+    } else {
+      ss = src_slot[e];
+    }
+    srcs[threadIdx.x] = ss;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    copy_rows(dst.p[4 * p + j], src.p[4 * p + j], geo.data_bytes[p], s0, rows, srcs);
+    if (geo.scale_bytes[p] > 0)
+      copy_rows(dst.p[4 * p + 2 + j], src.p[4 * p + 2 + j], geo.scale_bytes[p], s0, rows, srcs);
+  }
+  if (REUSE && stats != nullptr && threadIdx.x == 0 && (cnt[0] | cnt[1])) {
+    atomicAdd(stats, (unsigned long long)cnt[0]);
+    atomicAdd(stats + 1, (unsigned long long)cnt[1]);
+  }
+}
+
+// Block counts of a CopyLists launch; 0 for precisions with no destination bucket.
+int64_t copy_lists_setup(CopyLists& L, const int64_t* const* flat, const int64_t* counts,
+                         const Buckets& dst) {
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    L.flat[p] = flat[p];
+    L.n[p] = dst.p[4 * p] != nullptr ? counts[p] : 0;
+    acc += ceil_div(L.n[p], kListRows);
+    L.blk_end[p] = acc;
+  }
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
 // Paged store (PagedKVStore, shadowinfer/shadowkv/paged_kv_store.py). A page
 // holds one precision for tokens [start, start + n) of every (b, h) in
 // capacity buffers [B, H, P, ...]: payload rows of D values in the input
@@ -1547,6 +1666,57 @@ extern "C" int si_kv_compact(const int8_t* old_code, const int32_t* old_slot,
       old_code, old_slot, to_buckets(old_buckets), new_code, new_slot, to_buckets(new_buckets), n,
       geo);
   return check_launch("si_kv_compact");
+}
+
+extern "C" int si_kv_reuse_flat(const int64_t* const* cur_flat, const int64_t* cur_counts,
+                                void* const* cur_buckets, int64_t S, const int8_t* prev_code,
+                                const int32_t* prev_slot, const void* const* prev_buckets,
+                                int64_t S_prev, const uint8_t* mask, int64_t H, int64_t B,
+                                int64_t D, int64_t group, int scale_dtype, int64_t* stats,
+                                si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_reuse_flat: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(S >= 0 && S_prev >= 0 && H >= 0 && B >= 0 && D > 0, "si_kv_reuse_flat: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_reuse_flat: group must divide D");
+  if (S * H == 0 || S_prev == 0) return SI_OK;
+  SI_CHECK_ARG(cur_flat && cur_counts && cur_buckets && prev_code && prev_slot && prev_buckets && mask,
+               "si_kv_reuse_flat: NULL argument");
+  const Buckets dst = to_buckets(cur_buckets);
+  CopyLists L;
+  const int64_t blocks = copy_lists_setup(L, cur_flat, cur_counts, dst);
+  for (int p = 0; p < 4; ++p)
+    SI_CHECK_ARG(L.n[p] == 0 || L.flat[p] != nullptr, "si_kv_reuse_flat: NULL list %d", p);
+  if (blocks == 0) return SI_OK;
+  SI_CHECK_ARG(blocks < ((int64_t)1 << 31), "si_kv_reuse_flat: too many blocks");
+  kv_copy_lists<true><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+      L, dst, to_buckets(prev_buckets), prev_code, prev_slot, mask, S, H, S_prev,
+      make_geom(B, D, group, scale_dtype), reinterpret_cast<unsigned long long*>(stats));
+  return check_launch("si_kv_reuse_flat");
+}
+
+extern "C" int si_kv_compact_flat(const int32_t* old_slot, const void* const* old_buckets,
+                                  const int64_t* const* new_flat, const int64_t* new_counts,
+                                  void* const* new_buckets, int64_t S, int64_t H, int64_t B,
+                                  int64_t D, int64_t group, int scale_dtype, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_compact_flat: unsupported scale dtype %d",
+               scale_dtype);
+  SI_CHECK_ARG(S >= 0 && H >= 0 && B >= 0 && D > 0, "si_kv_compact_flat: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_compact_flat: group must divide D");
+  if (S * H == 0) return SI_OK;
+  SI_CHECK_ARG(old_slot && old_buckets && new_flat && new_counts && new_buckets,
+               "si_kv_compact_flat: NULL argument");
+  const Buckets dst = to_buckets(new_buckets);
+  CopyLists L;
+  const int64_t blocks = copy_lists_setup(L, new_flat, new_counts, dst);
+  for (int p = 0; p < 4; ++p)
+    SI_CHECK_ARG(L.n[p] == 0 || L.flat[p] != nullptr, "si_kv_compact_flat: NULL list %d", p);
+  if (blocks == 0) return SI_OK;
+  SI_CHECK_ARG(blocks < ((int64_t)1 << 31), "si_kv_compact_flat: too many blocks");
+  kv_copy_lists<false><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+      L, dst, to_buckets(old_buckets), nullptr, old_slot, nullptr, S, H, S,
+      make_geom(B, D, group, scale_dtype), nullptr);
+  return check_launch("si_kv_compact_flat");
 }
 
 extern "C" int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H,

@@ -58,6 +58,10 @@ _SIGNATURES = {
     "si_kv_reuse": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                            _i64, _i32, _vp, _vp]),
     "si_kv_compact": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "si_kv_reuse_flat": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                _i64, _i32, _vp, _vp]),
+    "si_kv_compact_flat": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
+                                  _vp]),
     "si_attn_workspace_bytes": (_sz, [_i64, _i64]),
     "si_attn_packed_fwd": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i64,
                                   _i64, ctypes.c_float, _vp, _i32, _vp, _sz, _vp]),

@@ -286,14 +286,26 @@ class PackedKVCache:
         return self._compute_data_bytes() + 48 * self.num_entries()
 
     # ----------------------------------------------------------------- evict
-    def evict(self, token_head_set: Set[Tuple[int, int]]) -> int:
+    def evict(self, token_head_set: Union[Set[Tuple[int, int]], torch.Tensor]) -> int:
         """Stable in-bucket compaction (packed_kv_cache.py:666-740); returns the
-        number of entries removed. Absent entries are never resurrected."""
-        if not token_head_set or not self._buckets:
-            return 0
-        mask = self._entry_mask(token_head_set.__iter__())
-        if mask is None:
-            return 0
+        number of entries removed. Absent entries are never resurrected.
+        Besides the reference's set of ``(t, h)`` pairs, a bool/uint8 ``[S, H]``
+        tensor marking the entries to evict is accepted (no host loop)."""
+        if torch.is_tensor(token_head_set):
+            if tuple(token_head_set.shape) not in ((self.seq_len, self.num_heads),
+                                                   (self.seq_len * self.num_heads,)):
+                raise ValueError(
+                    f"evict mask tensor must be [S, H], got {tuple(token_head_set.shape)}")
+            if not self._buckets:
+                return 0
+            mask = token_head_set.reshape(-1).to(device=self._grouping.code.device,
+                                                 dtype=torch.uint8).contiguous()
+        else:
+            if not token_head_set or not self._buckets:
+                return 0
+            mask = self._entry_mask(token_head_set.__iter__())
+            if mask is None:
+                return 0
         old = self._grouping
         dev = old.code.device
         new = DeviceGrouping.scan(old.code, evict_mask=mask.to(dev))
@@ -313,11 +325,13 @@ class PackedKVCache:
                 new_buckets[name] = fresh[name]
                 changed[name] = fresh[name]
         if changed:
-            _native.call("si_kv_compact", old.code.data_ptr(), old.slot.data_ptr(),
-                         self._bucket_table(), new.code.data_ptr(), new.slot.data_ptr(),
-                         self._bucket_table(changed), self.seq_len * self.num_heads,
-                         self.batch_size, self.head_dim, self._group_size,
-                         _native.dtype_code(self._scale_dtype), _native.stream(dev))
+            flat = new.flat_lists(self.seq_len, self.num_heads)
+            _native.call("si_kv_compact_flat", old.slot.data_ptr(), self._bucket_table(),
+                         _native.table4([f.data_ptr() for f in flat]),
+                         (ctypes.c_int64 * 5)(*new.counts), self._bucket_table(changed),
+                         self.seq_len, self.num_heads, self.batch_size, self.head_dim,
+                         self._group_size, _native.dtype_code(self._scale_dtype),
+                         _native.stream(dev))
         self._buckets = new_buckets
         self._grouping = new
         self._view = None
@@ -389,12 +403,15 @@ class PackedKVCache:
                 return stats if return_stats else None
             mask = host.to(dev)
         stats_dev = torch.zeros(2, dtype=torch.int64, device=dev) if return_stats else None
-        _native.call("si_kv_reuse", self._grouping.code.data_ptr(), self._grouping.slot.data_ptr(),
-                     self._bucket_table(), self.seq_len, prev._grouping.code.data_ptr(),
-                     prev._grouping.slot.data_ptr(), prev._bucket_table(), prev.seq_len,
-                     mask.data_ptr(), self.num_heads, self.batch_size, self.head_dim,
-                     self._group_size, _native.dtype_code(self._scale_dtype),
-                     _native.ptr(stats_dev), _native.stream(dev))
+        grouping = self._grouping
+        flat = grouping.flat_lists(self.seq_len, self.num_heads)
+        _native.call("si_kv_reuse_flat", _native.table4([f.data_ptr() for f in flat]),
+                     (ctypes.c_int64 * 5)(*grouping.counts), self._bucket_table(), self.seq_len,
+                     prev._grouping.code.data_ptr(), prev._grouping.slot.data_ptr(),
+                     prev._bucket_table(), prev.seq_len, mask.data_ptr(), self.num_heads,
+                     self.batch_size, self.head_dim, self._group_size,
+                     _native.dtype_code(self._scale_dtype), _native.ptr(stats_dev),
+                     _native.stream(dev))
         self._view = None
         if not return_stats:
             return None

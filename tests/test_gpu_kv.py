@@ -326,3 +326,78 @@ def test_codes_map_roundtrip_on_device_plan(dev):
     codes = mixed_codes(16, 4, seed=61, probs=(1, 1, 1, 1), evicted=0.2)
     plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
     assert codes_to_map(plan.codes) == codes_to_map(torch.from_numpy(codes))
+
+
+@pytest.mark.gpu
+def test_evict_tensor_mask_matches_set(dev):
+    """evict() with an [S, H] mask tensor equals evict() with the reference's
+    set of (t, h) pairs, and both equal the oracle's compaction."""
+    B, H, S, D = 2, 4, 70, 64
+    k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=9)
+    codes = mixed_codes(S, H, seed=9, probs=(1, 1, 1, 1), evicted=0.1)
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    a = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    b = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    m = np.random.default_rng(9).random((S, H)) < 0.3
+    pairs = {(int(t), int(h)) for t, h in zip(*np.nonzero(m))}
+    ref = oracle_pack(k, v, codes)
+    removed = O.kv_evict(ref, pairs)
+    assert a.evict(pairs) == removed
+    assert b.evict(torch.from_numpy(m).to(dev)) == removed
+    assert_cache_equal(a, ref)
+    assert_cache_equal(b, ref)
+    assert b.evict(torch.zeros(S, H, dtype=torch.bool, device=dev)) == 0
+    with pytest.raises(ValueError):
+        b.evict(torch.zeros(S, H + 1, dtype=torch.bool, device=dev))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (1, 8, 300, 128)),
+                                         (torch.float32, (2, 3, 50, 45))])
+def test_token_and_bucket_order_copies_agree(dev, dtype, shape):
+    """si_kv_reuse / si_kv_compact (token order) and si_kv_reuse_flat /
+    si_kv_compact_flat (bucket order, what PackedKVCache uses) write the same
+    buckets and the same stats."""
+    import ctypes
+    from shadowinfer_amd import _native
+    B, H, S, D = shape
+    k, v = kv_inputs(B, H, S, D, dtype, seed=S)
+    k2, v2 = kv_inputs(B, H, S, D, dtype, seed=S + 1)
+    codes = mixed_codes(S, H, seed=S, probs=(1, 1, 1, 1), evicted=0.1)
+    pcodes = codes.copy()
+    pcodes[np.random.default_rng(S).random((S, H)) < 0.3] = 2
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    pplan = PrecisionPlan.from_codes(torch.from_numpy(pcodes).to(dev))
+    prev = PackedKVCache.pack(k2.to(dev), v2.to(dev), None, plan=pplan)["packed_kv"]
+    a = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    b = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    mask = torch.from_numpy(np.random.default_rng(S + 2).random((S, H)) < 0.5).to(dev)
+    st_a = a.apply_reuse_mask(prev, mask, return_stats=True)       # bucket order
+    stats = torch.zeros(2, dtype=torch.int64, device=dev)
+    code, slot, _, sdt, g = b.device_state()
+    pcode, pslot, ptable, _, _ = prev.device_state()
+    _native.call("si_kv_reuse", code.data_ptr(), slot.data_ptr(), b._bucket_table(), S,
+                 pcode.data_ptr(), pslot.data_ptr(), ptable, S,
+                 mask.reshape(-1).to(torch.uint8).data_ptr(), H, B, D, g, sdt, stats.data_ptr(),
+                 _native.stream(dev))
+    assert st_a == {"applied": int(stats[0]), "skipped_precision": int(stats[1])}
+    for name, da in a.packed_data.items():
+        for key in ("k", "v", "scale_k", "scale_v"):
+            if da[key] is not None:
+                assert torch.equal(da[key], b.packed_data[name][key]), (name, key)
+    # compaction: the API (bucket order) against the token-order entry point
+    ev = torch.from_numpy(np.random.default_rng(S + 3).random((S, H)) < 0.25).to(dev)
+    old_code, old_slot, old_table, _, _ = b.device_state()
+    keep = {n: {kk: (t.clone() if torch.is_tensor(t) else t) for kk, t in d.items()}
+            for n, d in b._buckets.items()}
+    from shadowinfer_amd.shadowkv.precision_plan import DeviceGrouping
+    new = DeviceGrouping.scan(old_code, evict_mask=ev.reshape(-1).to(torch.uint8))
+    fresh = b._alloc_buckets(new.counts, dev, b._scale_dtype)
+    _native.call("si_kv_compact", old_code.data_ptr(), old_slot.data_ptr(), b._bucket_table(keep),
+                 new.code.data_ptr(), new.slot.data_ptr(), b._bucket_table(fresh), S * H, B, D, g,
+                 sdt, _native.stream(dev))
+    a.evict(ev)
+    for name, da in a._buckets.items():
+        for key in ("k", "v", "scale_k", "scale_v"):
+            if da.get(key) is not None:
+                assert torch.equal(da[key], fresh[name][key]), (name, key)
