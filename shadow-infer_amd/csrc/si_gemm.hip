@@ -801,7 +801,9 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             K_DMA8_256x128 = 16, K_DMA8_128x256 = 17,
             K_STREAM_N64 = 25, K_STREAM_N64_W8 = 27,
             // eight waves on a 128x128 tile (4x2 and 2x4 wave grids)
-            K_DMA8_128x128_42 = 30, K_DMA8_128x128_24 = 31 };
+            K_DMA8_128x128_42 = 30, K_DMA8_128x128_24 = 31,
+            // weight streaming with 32 / 16 output columns per block
+            K_STREAM_N32 = 32, K_STREAM_N16 = 33, K_STREAM_N32_W8 = 34, K_STREAM_N16_W8 = 35 };
 
 struct Plan {
   int kind;
@@ -838,7 +840,12 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   if (forced_kind() >= 0) {
     kind = forced_kind();
   } else if (M <= 32 && K % 64 == 0) {
-    kind = K_STREAM_N64;  // 4096 x 11008: M = 1 13 us, M = 16 14 us, M = 32 16 us
+    // Weight streaming; the column width per block sets how many CUs stream.
+    // M = 16: N = 11008 -> 64 columns (172 blocks, 12 us); N = 4096 -> 16
+    // columns, 8 waves (256 blocks: 12 us, 26.5 us with 64 columns); N = 22016
+    // -> 32 columns (688 blocks: 23.5 us, 27 us with 64).
+    const int64_t b64 = ceil_div(N, 64);
+    kind = b64 < 128 ? K_STREAM_N16_W8 : (b64 < 256 ? K_STREAM_N64 : K_STREAM_N32);
   } else if (K % 128 == 0) {
     // One tile per CU per wave of tiles. Estimated time = waves of 256 tiles
     // x (tile area / the tile's measured speed relative to 256x256); the
@@ -865,7 +872,8 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   if (kind == K_SKINNY) {
     if (M > 64 || K % 64 != 0) kind = K_TILE_128x128;
   }
-  if (kind == K_STREAM_N64 || kind == K_STREAM_N64_W8) {
+  if (kind == K_STREAM_N64 || kind == K_STREAM_N64_W8 || kind == K_STREAM_N32 ||
+      kind == K_STREAM_N16 || kind == K_STREAM_N32_W8 || kind == K_STREAM_N16_W8) {
     if (M > 64 || K % 64 != 0) {
       kind = K_TILE_128x128;
     } else {
@@ -980,8 +988,14 @@ void launch_stream(const Plan& p, const int8_t* a, const int8_t* b, int M, int N
 #define SI_STREAM(NF_, NW_, U_)                                                           \
   gemm_stream<MF, NF_, NW_, U_, EPI><<<dim3((unsigned)ceil_div(N, 16 * NF_)), dim3(64 * NW_), 0, st>>>( \
       a, b, M, N, K, c, ep)
-  if (p.kind == K_STREAM_N64_W8) SI_STREAM(4, 8, 2);
-  else SI_STREAM(4, 4, 4);
+  switch (p.kind) {
+    case K_STREAM_N64_W8: SI_STREAM(4, 8, 2); break;
+    case K_STREAM_N32: SI_STREAM(2, 4, 4); break;
+    case K_STREAM_N16: SI_STREAM(1, 4, 4); break;
+    case K_STREAM_N32_W8: SI_STREAM(2, 8, 2); break;
+    case K_STREAM_N16_W8: SI_STREAM(1, 8, 2); break;
+    default: SI_STREAM(4, 4, 4);
+  }
 #undef SI_STREAM
 }
 
@@ -989,7 +1003,8 @@ template <int EPI>
 void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
             const EpiArgs& ep, hipStream_t st) {
   const dim3 block(256);
-  if (p.kind == K_STREAM_N64 || p.kind == K_STREAM_N64_W8) {
+  if (p.kind == K_STREAM_N64 || p.kind == K_STREAM_N64_W8 || p.kind == K_STREAM_N32 ||
+      p.kind == K_STREAM_N16 || p.kind == K_STREAM_N32_W8 || p.kind == K_STREAM_N16_W8) {
     switch (p.mf) {
       case 1: launch_stream<1, EPI>(p, a, b, M, N, K, c, ep, st); break;
       case 2: launch_stream<2, EPI>(p, a, b, M, N, K, c, ep, st); break;

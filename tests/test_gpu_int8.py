@@ -52,7 +52,8 @@ def _exact_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 @pytest.mark.parametrize("M,K,N", [(1, 64, 16), (5, 128, 96), (16, 4096, 11008),
                                    (64, 4096, 11008), (33, 256, 48), (300, 512, 272),
                                    (7, 40, 24), (3, 17, 5), (100, 96, 48), (65, 4096, 200),
-                                   (900, 1024, 300), (17, 11008, 4096)])
+                                   (900, 1024, 300), (17, 11008, 4096), (16, 11008, 4096),
+                                   (16, 4096, 22016), (3, 512, 5000)])
 def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
     g = torch.Generator().manual_seed(M * 7 + K + N)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
