@@ -326,6 +326,14 @@ int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H,
                   int64_t D, int64_t t0, int64_t take, int precision, int64_t group,
                   void* const* page, int64_t capacity, int64_t offset, si_stream_t stream);
 
+/* si_page_write for a run of n_pages fresh pages allocated page-major (page i
+ * at pages[x] + i * its bytes per page, each page [B, H, capacity, ...]): tokens
+ * t0 .. t0 + n_pages * capacity - 1 fill pages 0 .. n_pages - 1 in order, as
+ * n_pages appends of whole pages would (paged_kv_store.py:248-307). */
+int si_page_write_pages(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t T,
+                        int64_t D, int64_t t0, int64_t n_pages, int precision, int64_t group,
+                        void* const* pages, int64_t capacity, si_stream_t stream);
+
 /* Replaces PagedKVStore.gather / _decode (paged_kv_store.py:326-405): every
  * page of the device table (int64 [n_pages, 8] rows {precision, k, v,
  * scale_k, scale_v, start token, tokens, capacity}) decoded into fp32

@@ -1297,7 +1297,9 @@ __global__ __launch_bounds__(256) void page_write_fast(const void* __restrict__ 
   if (j >= take) return;
   const int64_t bh = blockIdx.y;
   const int64_t src = (bh * T + t0 + j) * D + lane * EPL;
-  const int dst = (int)(bh * P + off + j);
+  // Row off + j of (b, h) in a run of pages of P rows each, B*H*P rows per page.
+  const int r = off + j;
+  const int dst = (r / P) * ((int)gridDim.y * P) + (int)bh * P + r % P;
   if (prec == SI_PREC_FP32) {  // the input dtype, unchanged
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + src * ES);
@@ -1326,7 +1328,8 @@ __global__ __launch_bounds__(256) void page_write_generic(const void* __restrict
     const int64_t bh = r / take;
     const int64_t j = r - bh * take;
     const int64_t src = (bh * T + t0 + j) * D;
-    const int64_t dst = bh * P + off + j;
+    const int64_t rr = off + j;  // row of (b, h) in a run of pages of P rows each
+    const int64_t dst = (rr / P) * (BH * P) + bh * P + rr % P;
     if (prec == SI_PREC_FP32) {
       for (int64_t d = 0; d < D * ES; ++d) {
         reinterpret_cast<char*>(pg.p[0])[dst * D * ES + d] = reinterpret_cast<const char*>(kin)[src * ES + d];
@@ -1719,25 +1722,26 @@ extern "C" int si_kv_compact_flat(const int32_t* old_slot, const void* const* ol
   return check_launch("si_kv_compact_flat");
 }
 
-extern "C" int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H,
-                             int64_t T, int64_t D, int64_t t0, int64_t take, int precision,
-                             int64_t group, void* const* page, int64_t capacity, int64_t offset,
-                             si_stream_t stream) {
-  clear_error();
+namespace {
+int page_write_run(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t T,
+                   int64_t D, int64_t t0, int64_t take, int precision, int64_t group,
+                   void* const* page, int64_t capacity, int64_t offset, int64_t n_pages,
+                   si_stream_t stream) {
   SI_CHECK_ARG(dtype_ok(dtype), "si_page_write: unsupported dtype %d", dtype);
   SI_CHECK_ARG(precision >= SI_PREC_FP32 && precision <= SI_PREC_INT4,
                "si_page_write: precision %d is not 0..3", precision);
   SI_CHECK_ARG(B >= 0 && H >= 0 && T >= 0 && D > 0 && take >= 0 && t0 >= 0 && t0 + take <= T,
                "si_page_write: tokens [%lld, %lld) outside [0, %lld)", (long long)t0,
                (long long)(t0 + take), (long long)T);
-  SI_CHECK_ARG(offset >= 0 && offset + take <= capacity,
-               "si_page_write: rows [%lld, %lld) outside the page capacity %lld",
-               (long long)offset, (long long)(offset + take), (long long)capacity);
+  SI_CHECK_ARG(n_pages >= 1 && capacity > 0 && offset >= 0 && offset + take <= capacity * n_pages,
+               "si_page_write: rows [%lld, %lld) outside %lld page(s) of %lld rows",
+               (long long)offset, (long long)(offset + take), (long long)n_pages,
+               (long long)capacity);
   SI_CHECK_ARG(group > 0 && D % group == 0, "si_page_write: group must divide D");
   if (B * H * take == 0) return SI_OK;
   SI_CHECK_ARG(k && v && page && page[0] && page[1], "si_page_write: NULL argument");
   SI_CHECK_ARG(precision < SI_PREC_INT8 || (page[2] && page[3]), "si_page_write: NULL scales");
-  SI_CHECK_ARG(B * H < 65536 && B * H * capacity < ((int64_t)1 << 31),
+  SI_CHECK_ARG(B * H < 65536 && B * H * capacity * n_pages < ((int64_t)1 << 31),
                "si_page_write: store too large for one launch");
   Buckets pg = to_buckets(nullptr);
   const int base = precision == SI_PREC_FP32 ? 0 : 4 * precision;
@@ -1780,6 +1784,25 @@ extern "C" int si_page_write(const void* k, const void* v, int dtype, int64_t B,
   else
     page_write_generic<SI_DT_BF16><<<grid, 256, 0, st>>>(k, v, B * H, T, D, t0, take, capacity, offset, precision, group, pg);
   return check_launch("si_page_write/generic");
+}
+}  // namespace
+
+extern "C" int si_page_write(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                             int64_t T, int64_t D, int64_t t0, int64_t take, int precision,
+                             int64_t group, void* const* page, int64_t capacity, int64_t offset,
+                             si_stream_t stream) {
+  clear_error();
+  return page_write_run(k, v, dtype, B, H, T, D, t0, take, precision, group, page, capacity,
+                        offset, 1, stream);
+}
+
+extern "C" int si_page_write_pages(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                                   int64_t T, int64_t D, int64_t t0, int64_t n_pages,
+                                   int precision, int64_t group, void* const* pages,
+                                   int64_t capacity, si_stream_t stream) {
+  clear_error();
+  return page_write_run(k, v, dtype, B, H, T, D, t0, n_pages * capacity, precision, group, pages,
+                        capacity, 0, n_pages, stream);
 }
 
 extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, int64_t B,

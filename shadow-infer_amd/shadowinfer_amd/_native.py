@@ -51,6 +51,8 @@ _SIGNATURES = {
                                _vp, _vp, _vp, _vp, _vp]),
     "si_page_write": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _vp,
                              _i64, _i64, _vp]),
+    "si_page_write_pages": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
+                                   _vp, _i64, _vp]),
     "si_page_gather": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_kv_unpack_flat": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp,
                                  _vp, _vp]),

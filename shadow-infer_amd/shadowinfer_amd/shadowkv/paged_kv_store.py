@@ -149,27 +149,29 @@ class PagedKVStore:
                 f"{tuple(k_new.shape)}")
 
     # ------------------------------------------------------------------ buffers
-    def _new_buffers(self, precision: str, dtype: torch.dtype, dev) -> Dict[str, Optional[torch.Tensor]]:
+    def _new_buffers(self, precision: str, dtype: torch.dtype, dev,
+                     count: Optional[int] = None) -> Dict[str, Optional[torch.Tensor]]:
+        """Capacity buffers of one page, or of ``count`` pages allocated
+        together (a leading page dimension; page i is ``buf[name][i]``)."""
         B, H, P, D = self.batch_size, self.num_heads, self.page_size, self.head_dim
+        lead = () if count is None else (count,)
+
+        def empty(*shape, dt):
+            return torch.empty(*lead, *shape, dtype=dt, device=dev)
+
         if precision == "fp32":
-            return {"k": torch.empty(B, H, P, D, dtype=dtype, device=dev),
-                    "v": torch.empty(B, H, P, D, dtype=dtype, device=dev),
+            return {"k": empty(B, H, P, D, dt=dtype), "v": empty(B, H, P, D, dt=dtype),
                     "scale_k": None, "scale_v": None}
         if precision == "fp16":
-            return {"k": torch.empty(B, H, P, D, dtype=torch.float16, device=dev),
-                    "v": torch.empty(B, H, P, D, dtype=torch.float16, device=dev),
-                    "scale_k": None, "scale_v": None}
+            return {"k": empty(B, H, P, D, dt=torch.float16),
+                    "v": empty(B, H, P, D, dt=torch.float16), "scale_k": None, "scale_v": None}
         if precision == "int8":
-            return {"k": torch.empty(B, H, P, D, dtype=torch.int8, device=dev),
-                    "v": torch.empty(B, H, P, D, dtype=torch.int8, device=dev),
-                    "scale_k": torch.empty(B, H, P, 1, dtype=dtype, device=dev),
-                    "scale_v": torch.empty(B, H, P, 1, dtype=dtype, device=dev)}
+            return {"k": empty(B, H, P, D, dt=torch.int8), "v": empty(B, H, P, D, dt=torch.int8),
+                    "scale_k": empty(B, H, P, 1, dt=dtype), "scale_v": empty(B, H, P, 1, dt=dtype)}
         G = D // self._int4_effective_group
         rb = (D + 1) // 2
-        return {"k": torch.empty(B, H, P, rb, dtype=torch.uint8, device=dev),
-                "v": torch.empty(B, H, P, rb, dtype=torch.uint8, device=dev),
-                "scale_k": torch.empty(B, H, P, G, 1, dtype=dtype, device=dev),
-                "scale_v": torch.empty(B, H, P, G, 1, dtype=dtype, device=dev)}
+        return {"k": empty(B, H, P, rb, dt=torch.uint8), "v": empty(B, H, P, rb, dt=torch.uint8),
+                "scale_k": empty(B, H, P, G, 1, dt=dtype), "scale_v": empty(B, H, P, G, 1, dt=dtype)}
 
     def _write(self, page: _Page, k: torch.Tensor, v: torch.Tensor, t0: int, take: int,
                offset: int) -> None:
@@ -204,6 +206,12 @@ class PagedKVStore:
         cursor = 0
         while cursor < tokens:
             open_slot = self._open_slot(precision)
+            full = (tokens - cursor) // self.page_size
+            if open_slot is None and full >= 2:
+                # a run of whole new pages: one allocation per buffer, one launch
+                self._append_pages(k, v, cursor, full, precision)
+                cursor += full * self.page_size
+                continue
             if open_slot is None:
                 capacity = self.page_size
             else:
@@ -226,6 +234,24 @@ class PagedKVStore:
             cursor += take
             self._max_seq += take
         self._appended_tokens += tokens
+
+    def _append_pages(self, k: torch.Tensor, v: torch.Tensor, t0: int, count: int,
+                      precision: str) -> None:
+        """``count`` sealed pages holding tokens [t0, t0 + count * page_size)."""
+        B, H, T, D = k.shape
+        P = self.page_size
+        bufs = self._new_buffers(precision, k.dtype, k.device, count=count)
+        ptrs = [bufs[n].data_ptr() if bufs[n] is not None else None
+                for n in ("k", "v", "scale_k", "scale_v")]
+        _native.call("si_page_write_pages", k.data_ptr(), v.data_ptr(), _native.dtype_code(k.dtype),
+                     B, H, T, D, t0, count, _PREC_CODE[precision], self._int4_effective_group,
+                     _native.table4(ptrs), P, _native.stream(k.device))
+        for i in range(count):
+            slot = self._alloc_slot()
+            self._order.append(slot)
+            buf = {n: (None if t is None else t[i]) for n, t in bufs.items()}
+            self.pages[slot] = _Page(precision, buf, self._max_seq, P, True)
+            self._max_seq += P
 
     def _seal_tail(self) -> None:
         if self._order:

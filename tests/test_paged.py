@@ -295,3 +295,31 @@ def test_layer_sized_prefill_matches_packed_cache(dev):
     ref = PackedKVCache.pack(k, v, None, plan=PrecisionPlan.from_codes(codes))["packed_kv"]
     rk, rv = ref.unpack()
     assert torch.equal(gk, rk) and torch.equal(gv, rv)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("precision", ["fp32", "fp16", "int8", "int4"])
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 32), (torch.float32, 32), (torch.bfloat16, 45)])
+def test_page_runs_equal_page_by_page(dev, precision, dtype, d):
+    """One append of several whole pages (one allocation, si_page_write_pages)
+    leaves the same pages as appending them one page at a time, including
+    after a partly filled open page."""
+    k, v = _kv(21, s=43, d=d, dtype=dtype)
+    a, b = _store(dev, d=d), _store(dev, d=d)
+    a.append(k[:, :, :3].to(dev), v[:, :, :3].to(dev), precision)      # open page of 3
+    a.append(k[:, :, 3:].to(dev), v[:, :, 3:].to(dev), precision)      # fills it, 4 whole pages, tail
+    _append(b, k, v, precision, split=(3, 5, 8, 8, 8, 8, 3), dev=dev)
+    assert a.page_count == b.page_count == 6
+    for pa, pb in zip(a.pages, b.pages):
+        assert (pa.start_token, pa.num_tokens, pa.sealed) == (pb.start_token, pb.num_tokens, pb.sealed)
+        for name in ("k", "v", "scale_k", "scale_v"):
+            ta, tb = getattr(pa, name), getattr(pb, name)
+            assert (ta is None) == (tb is None)
+            if ta is not None:
+                assert ta.shape == tb.shape and torch.equal(ta, tb), name
+    ga, gb = a.gather(), b.gather()
+    assert torch.equal(ga[0], gb[0]) and torch.equal(ga[1], gb[1])
+    wk, wv = _golden(k, v, precision)
+    _eq(ga[0], wk)
+    _eq(ga[1], wv)
+    assert a.data_plane_bytes() == b.data_plane_bytes()
