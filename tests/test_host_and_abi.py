@@ -232,3 +232,46 @@ def test_packed_attention_validation():
         packed_attention(torch.randn(8, 64, dtype=torch.bfloat16), cache)
     with pytest.raises(TypeError):
         packed_attention(torch.randn(1, 2, 8, 64), cache)
+
+
+def test_step_and_copy_entry_points_reject_bad_arguments():
+    """The denoising-step row kernels, the bucket-order copies, the page-run
+    writer and the prebuilt-list attention reject invalid arguments before any
+    HIP call (status 1 and a message; no device needed)."""
+    lib = _native.load()
+    null = None
+    t4 = _native.table4([None] * 4)
+    t16 = _native.table16([None] * 16)
+    c5 = (ctypes.c_int64 * 5)(0, 1, 0, 0, 0)
+    f = ctypes.c_float
+    checks = [
+        # K not a multiple of 8 / above the register budget / q without scale
+        (lambda: lib.si_rmsnorm_rows(16, 2, 4, 12, 16, f(1e-5), 16, null, null, null), b"multiple of 8"),
+        (lambda: lib.si_rmsnorm_rows(16, 2, 4, 32768, 16, f(1e-5), 16, null, null, null), b"multiple of 8"),
+        (lambda: lib.si_rmsnorm_rows(16, 2, 4, 64, 16, f(1e-5), null, 16, null, null), b"together"),
+        (lambda: lib.si_rmsnorm_rows(16, 9, 4, 64, 16, f(1e-5), 16, null, null, null), b"dtype"),
+        (lambda: lib.si_rmsnorm_rows(8, 2, 4, 64, 16, f(1e-5), 16, null, null, null), b"aligned"),
+        (lambda: lib.si_rope_split(16, 2, 1, 8, 4, 96, 16, 16, 16, 16, 16, null), b"head_dim"),
+        (lambda: lib.si_rope_split(16, 2, 1, 8, 4, 64, 16, 16, null, 16, 16, null), b"NULL"),
+        (lambda: lib.si_swiglu_quant(16, 2, 4, 12, null, 16, 16, null), b"multiple of 8"),
+        (lambda: lib.si_swiglu_quant(16, 2, 4, 64, null, null, 16, null), b"NULL"),
+        (lambda: lib.si_row_argmax_conf(16, 2, 4, 0, 16, 16, null), b"shape"),
+        (lambda: lib.si_row_argmax_conf(16, 7, 4, 8, 16, 16, null), b"dtype"),
+        (lambda: lib.si_kv_reuse_flat(t4, c5, t16, 8, 1, 1, t16, 8, 1, 2, 1, 64, 48, 2, null, null), b"group"),
+        (lambda: lib.si_kv_reuse_flat(t4, c5, t16, 8, 1, 1, t16, 8, null, 2, 1, 64, 16, 2, null, null), b"NULL"),
+        (lambda: lib.si_kv_compact_flat(1, t16, t4, c5, t16, 8, 2, 1, 64, 16, 9, null), b"scale dtype"),
+        (lambda: lib.si_page_write_pages(16, 16, 2, 1, 2, 8, 64, 0, 2, 2, 16, t4, 8, null), b"outside"),
+        (lambda: lib.si_page_write_pages(16, 16, 2, 1, 2, 64, 64, 0, 2, 5, 16, t4, 8, null), b"precision"),
+        (lambda: lib.si_attn_build_lists(1, 1, 2, 64, 16, 7, null), b"workspace"),
+        (lambda: lib.si_attn_packed_fwd_built(16, 2, 1, 2, 8, 96, 16, 1 << 20, t16, 2, 64, 16, f(0.1), 16, 0,
+                                      0, null), b"head_dim"),
+    ]
+    for call, word in checks:
+        rc = call()
+        msg = lib.si_last_error()
+        assert rc == 1 and word in msg, (rc, msg, word)
+    # zero-sized work is a no-op that succeeds
+    assert lib.si_rmsnorm_rows(null, 2, 0, 64, null, f(1e-5), null, null, null, null) == 0
+    assert lib.si_swiglu_quant(null, 2, 0, 64, null, null, null, null) == 0
+    assert lib.si_rope_split(null, 2, 0, 8, 4, 64, null, null, null, null, null, null) == 0
+    assert lib.si_kv_compact_flat(1, t16, t4, c5, t16, 0, 2, 1, 64, 16, 2, null) == 0
