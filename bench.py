@@ -302,9 +302,16 @@ def bench_gemm(torch, dev, iters=50):
     K, N = 4096, 11008
     gen = torch.Generator(device=dev).manual_seed(7)
     copies = 8  # 8 x 45 MB of weights: more than the 256 MB last-level cache
-    ws = [torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
-          for _ in range(copies)]  # [N, K]: nn.Linear layout, as INT8Linear keeps it
-    sw = torch.rand(N, generator=gen, device=dev) * 1e-3 + 1e-4
+    # W ~ N(0, 0.02) quantized per output channel (INT8Linear.from_linear's
+    # arithmetic, si_weight_quant_i8), kept in nn.Linear's [N, K] layout.
+    ws = []
+    sw = torch.empty(N, dtype=torch.float32, device=dev)
+    for _ in range(copies):
+        w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+        q = torch.empty(N, K, dtype=torch.int8, device=dev)
+        _native.call("si_weight_quant_i8", w.data_ptr(), N, K, q.data_ptr(), sw.data_ptr(), sptr)
+        ws.append(q)
+        del w
     timer = EventTimer(torch, stream)
     out = {}
     for M in (16, 64, 256, 1024):

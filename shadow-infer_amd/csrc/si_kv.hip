@@ -404,6 +404,14 @@ __device__ __forceinline__ uint32_t codes_bf16x2(uint32_t q0, uint32_t q1) {
   return a | b;
 }
 
+// Bucket row stores of the bf16 pack. Plain (cached) stores: a non-temporal
+// store made the pack 3% faster but pushed the buckets out of the last-level
+// cache, and an unpack that follows the pack then took 23% longer.
+template <typename T>
+__device__ __forceinline__ void st_row(void* p, T v) {
+  *reinterpret_cast<T*>(p) = v;
+}
+
 template <int LPR, bool WC>
 __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32_t wv[4], int c,
                                               int s, int b, int B, int lane, int lpg,
@@ -421,8 +429,15 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
       xv[2 * i + 1] = __uint_as_float(wv[i] & 0xffff0000u);
     }
     if (c == SI_PREC_FP16) {
-      store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, xk);
-      store_f16<8>(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, xv);
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      u32x4 hk, hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hk[i] = f32_to_f16_bits(xk[2 * i]) | (f32_to_f16_bits(xk[2 * i + 1]) << 16);
+        hv[i] = f32_to_f16_bits(xv[2 * i]) | (f32_to_f16_bits(xv[2 * i + 1]) << 16);
+      }
+      st_row(reinterpret_cast<uint16_t*>(bk.p[4]) + oel, hk);
+      st_row(reinterpret_cast<uint16_t*>(bk.p[5]) + oel, hv);
       if constexpr (WC) {
         float fk[8], fv[8];
 #pragma unroll
@@ -476,10 +491,11 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
     }
   }
   if (i8) {
-    *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(bk.p[8]) + oel) =
-        make_uint2(bytes4(qk[0], qk[1], qk[2], qk[3]), bytes4(qk[4], qk[5], qk[6], qk[7]));
-    *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(bk.p[9]) + oel) =
-        make_uint2(bytes4(qv[0], qv[1], qv[2], qv[3]), bytes4(qv[4], qv[5], qv[6], qv[7]));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    st_row(reinterpret_cast<int8_t*>(bk.p[8]) + oel,
+           u32x2{bytes4(qk[0], qk[1], qk[2], qk[3]), bytes4(qk[4], qk[5], qk[6], qk[7])});
+    st_row(reinterpret_cast<int8_t*>(bk.p[9]) + oel,
+           u32x2{bytes4(qv[0], qv[1], qv[2], qv[3]), bytes4(qv[4], qv[5], qv[6], qv[7])});
     if (lane == 0) {
       reinterpret_cast<uint16_t*>(bk.p[10])[orow] = (uint16_t)(__float_as_uint(sk) >> 16);
       reinterpret_cast<uint16_t*>(bk.p[11])[orow] = (uint16_t)(__float_as_uint(sv) >> 16);
@@ -495,10 +511,8 @@ __device__ __forceinline__ void pack_row_bf16(const uint32_t wk[4], const uint32
     }
     const int64_t rb = (int64_t)B * D / 2;
     const int64_t boff = (int64_t)s * rb + ((int64_t)b * D + lane * 8) / 2;
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(bk.p[12]) + boff) =
-        bytes4(bkk[0], bkk[1], bkk[2], bkk[3]) ^ 0x88888888u;
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(bk.p[13]) + boff) =
-        bytes4(bvv[0], bvv[1], bvv[2], bvv[3]) ^ 0x88888888u;
+    st_row(reinterpret_cast<uint8_t*>(bk.p[12]) + boff, bytes4(bkk[0], bkk[1], bkk[2], bkk[3]) ^ 0x88888888u);
+    st_row(reinterpret_cast<uint8_t*>(bk.p[13]) + boff, bytes4(bvv[0], bvv[1], bvv[2], bvv[3]) ^ 0x88888888u);
     if ((lane & (lpg - 1)) == 0) {
       const int64_t si = orow * (LPR / lpg) + lane / lpg;
       reinterpret_cast<uint16_t*>(bk.p[14])[si] = (uint16_t)(__float_as_uint(sk) >> 16);
@@ -615,14 +629,14 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
 // one precision's bucket (the flat index lists give each row's dense row
 // b*H*S + h*S + t), so every wave quantizes a single precision and the bucket
 // rows are written contiguously. blk_end[p]: first block after precision p's.
-template <int DT, int LPR, int U, int P>
+template <int DT, int LPR, int U, int P, int NT>
 __device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
                                                  const void* __restrict__ vin,
                                                  const UnpackLists& L, int64_t lb, int B,
                                                  int64_t HS, int lpg, const Buckets& bk) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int D = EPL * LPR;
-  constexpr int RPP = 256 / LPR;
+  constexpr int RPP = NT / LPR;
   const int lane = threadIdx.x % LPR;
   const int64_t rows = L.n[P] * B;
   const int64_t r0 = lb * (RPP * U) + threadIdx.x / LPR;
@@ -677,20 +691,20 @@ __device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
   }
 }
 
-template <int DT, int LPR, int U>
-__global__ __launch_bounds__(256) void kv_pack_lists(const void* __restrict__ kin,
+template <int DT, int LPR, int U, int NT>
+__global__ __launch_bounds__(NT) void kv_pack_lists(const void* __restrict__ kin,
                                                      const void* __restrict__ vin, UnpackLists L,
                                                      int B, int H, int S, int lpg, Buckets bk) {
   const int64_t blk = blockIdx.x;
   const int64_t HS = (int64_t)H * S;
   if (blk < L.blk_end[0]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_FP32>(kin, vin, L, blk, B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP32, NT>(kin, vin, L, blk, B, HS, lpg, bk);
   } else if (blk < L.blk_end[1]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_FP16>(kin, vin, L, blk - L.blk_end[0], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP16, NT>(kin, vin, L, blk - L.blk_end[0], B, HS, lpg, bk);
   } else if (blk < L.blk_end[2]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_INT8>(kin, vin, L, blk - L.blk_end[1], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT8, NT>(kin, vin, L, blk - L.blk_end[1], B, HS, lpg, bk);
   } else {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_INT4>(kin, vin, L, blk - L.blk_end[2], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT4, NT>(kin, vin, L, blk - L.blk_end[2], B, HS, lpg, bk);
   }
 }
 
@@ -935,12 +949,12 @@ __global__ __launch_bounds__(256) void kv_unpack_sorted(const int8_t* __restrict
 // Blocks past the buckets zero the rows of entries whose code is outside
 // 0..3 (evicted or absent). blk_end[p]: first block after precision p's.
 
-template <int D, int SDT, int U, int P>
+template <int D, int SDT, int U, int P, int NT>
 __device__ __forceinline__ void unpack_bucket_rows(const UnpackLists& L, const Buckets& bk,
                                                    int64_t lb, int B, int64_t HS, int g,
                                                    float* __restrict__ ok, float* __restrict__ ov) {
   constexpr int CPR = D / 4;
-  constexpr int RPP = 256 / CPR;
+  constexpr int RPP = NT / CPR;
   const int ch = threadIdx.x % CPR;
   const int64_t rows = L.n[P] * B;
   const int64_t r0 = lb * (RPP * U) + threadIdx.x / CPR;
@@ -970,8 +984,8 @@ __device__ __forceinline__ void unpack_bucket_rows(const UnpackLists& L, const B
   }
 }
 
-template <int D, int SDT, int U>
-__global__ __launch_bounds__(256) void kv_unpack_lists(UnpackLists L,
+template <int D, int SDT, int U, int NT>
+__global__ __launch_bounds__(NT) void kv_unpack_lists(UnpackLists L,
                                                        const int8_t* __restrict__ code,
                                                        Buckets bk, int B, int H, int S, int g,
                                                        float* __restrict__ ok,
@@ -980,19 +994,19 @@ __global__ __launch_bounds__(256) void kv_unpack_lists(UnpackLists L,
   const int64_t HS = (int64_t)H * S;
   if (blk < L.blk_end[3]) {
     if (blk < L.blk_end[0]) {
-      unpack_bucket_rows<D, SDT, U, SI_PREC_FP32>(L, bk, blk, B, HS, g, ok, ov);
+      unpack_bucket_rows<D, SDT, U, SI_PREC_FP32, NT>(L, bk, blk, B, HS, g, ok, ov);
     } else if (blk < L.blk_end[1]) {
-      unpack_bucket_rows<D, SDT, U, SI_PREC_FP16>(L, bk, blk - L.blk_end[0], B, HS, g, ok, ov);
+      unpack_bucket_rows<D, SDT, U, SI_PREC_FP16, NT>(L, bk, blk - L.blk_end[0], B, HS, g, ok, ov);
     } else if (blk < L.blk_end[2]) {
-      unpack_bucket_rows<D, SDT, U, SI_PREC_INT8>(L, bk, blk - L.blk_end[1], B, HS, g, ok, ov);
+      unpack_bucket_rows<D, SDT, U, SI_PREC_INT8, NT>(L, bk, blk - L.blk_end[1], B, HS, g, ok, ov);
     } else {
-      unpack_bucket_rows<D, SDT, U, SI_PREC_INT4>(L, bk, blk - L.blk_end[2], B, HS, g, ok, ov);
+      unpack_bucket_rows<D, SDT, U, SI_PREC_INT4, NT>(L, bk, blk - L.blk_end[2], B, HS, g, ok, ov);
     }
     return;
   }
   // zero rows: entries e = t*H + h with a code outside 0..3
   constexpr int CPR = D / 4;
-  constexpr int RPP = 256 / CPR;
+  constexpr int RPP = NT / CPR;
   const int ch = threadIdx.x % CPR;
   const int64_t e0 = (blk - L.blk_end[3]) * (RPP * U) + threadIdx.x / CPR;
   typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -1481,7 +1495,10 @@ int launch_pack(const void* k, const void* v, int64_t B, int64_t H, int64_t S, i
                 int64_t g, const int8_t* code, const int32_t* slot, const Buckets& bk,
                 const WorkCopy& wc, hipStream_t st) {
   constexpr int EPL = Chunk<DT>::EPL;
-  constexpr int U = 2;
+#ifndef SI_PACK_FAST_U
+#define SI_PACK_FAST_U 1
+#endif
+  constexpr int U = SI_PACK_FAST_U;
   const int64_t lpr = D / EPL;
   const int64_t lpg = g / EPL;
   const bool aligned = ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
@@ -1862,8 +1879,20 @@ extern "C" int si_kv_unpack_flat(const int8_t* code, const int32_t* slot,
   if (!(vec && small && (D == 128 || D == 64)))  // other shapes: the token-order kernels
     return si_kv_unpack(code, slot, buckets, scale_dtype, B, H, S, D, group, out_k, out_v, stream);
   const Buckets bk = to_buckets(buckets);
-  constexpr int U = 4;
-  const int64_t rpb = (256 / (D / 4)) * U;
+  // Rows per thread (U) and threads per block (NT) of the bucket-order pack and
+  // unpack are compile-time constants (-D overrides for tuning builds). On a
+  // 7B-shaped layer one row per thread is fastest: unpack 55.8 us (U = 2:
+  // 55.9, 4: 58.8, 8: 62.3), pack 43.2 us (U = 2: 46.1, 4: 49.4, 8: 56.5);
+  // 64- to 512-thread blocks are within 2% of each other.
+#ifndef SI_UNPACK_LISTS_U
+#define SI_UNPACK_LISTS_U 1
+#endif
+  constexpr int U = SI_UNPACK_LISTS_U;
+#ifndef SI_UNPACK_LISTS_NT
+#define SI_UNPACK_LISTS_NT 256
+#endif
+  constexpr int NT = SI_UNPACK_LISTS_NT;
+  const int64_t rpb = (NT / (D / 4)) * U;
   UnpackLists L;
   int64_t acc = 0;
   for (int p = 0; p < 4; ++p) {
@@ -1878,7 +1907,7 @@ extern "C" int si_kv_unpack_flat(const int8_t* code, const int32_t* slot,
   const dim3 grid((unsigned)L.blk_end[4]);
   hipStream_t st = as_stream(stream);
 #define SI_UL(D_, SDT_) \
-  kv_unpack_lists<D_, SDT_, U><<<grid, 256, 0, st>>>(L, code, bk, (int)B, (int)H, (int)S, (int)group, out_k, out_v)
+  kv_unpack_lists<D_, SDT_, U, NT><<<grid, NT, 0, st>>>(L, code, bk, (int)B, (int)H, (int)S, (int)group, out_k, out_v)
   if (D == 128) {
     if (scale_dtype == SI_DT_F32) SI_UL(128, SI_DT_F32);
     else if (scale_dtype == SI_DT_F16) SI_UL(128, SI_DT_F16);
@@ -1922,8 +1951,15 @@ extern "C" int si_kv_pack_flat(const void* k, const void* v, int dtype, int64_t 
   const bool fast = aligned && D % epl == 0 && pow2(lpr) && lpr >= 4 && lpr <= 64 &&
                     group % epl == 0 && pow2(lpg) && lpg <= lpr && B * H * S < ((int64_t)1 << 31);
   if (!fast) return si_kv_pack(k, v, dtype, B, H, S, D, group, code, slot, buckets, stream);
-  constexpr int U = 2;
-  const int64_t rpb = (256 / lpr) * U;
+#ifndef SI_PACK_LISTS_U
+#define SI_PACK_LISTS_U 1
+#endif
+  constexpr int U = SI_PACK_LISTS_U;
+#ifndef SI_PACK_LISTS_NT
+#define SI_PACK_LISTS_NT 256
+#endif
+  constexpr int NT = SI_PACK_LISTS_NT;
+  const int64_t rpb = (NT / lpr) * U;
   UnpackLists L;
   int64_t acc = 0;
   for (int p = 0; p < 4; ++p) {
@@ -1937,7 +1973,7 @@ extern "C" int si_kv_pack_flat(const void* k, const void* v, int dtype, int64_t 
   SI_CHECK_ARG(acc < ((int64_t)1 << 31), "si_kv_pack_flat: too many blocks");
   const dim3 grid((unsigned)acc);
 #define SI_PL(DT_, L_) \
-  kv_pack_lists<DT_, L_, U><<<grid, 256, 0, st>>>(k, v, L, (int)B, (int)H, (int)S, (int)lpg, bk)
+  kv_pack_lists<DT_, L_, U, NT><<<grid, NT, 0, st>>>(k, v, L, (int)B, (int)H, (int)S, (int)lpg, bk)
 #define SI_PL_DT(DT_)               \
   switch (lpr) {                    \
     case 4: SI_PL(DT_, 4); break;   \
