@@ -18,7 +18,8 @@
 //
 // Precision: fp16 operands (10-bit mantissa) with fp32 accumulation and an
 // fp32 online softmax; fp16 entries of the cache are exact in fp16, int8/int4
-// values q*s are rounded once to fp16.
+// values q*s are rounded once to fp16, and P is rounded to fp16 for the P.V
+// MFMAs (its row sum adds the same fp16 values).
 #include <type_traits>
 
 #include "si_kv_common.h"
@@ -29,6 +30,7 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int BN = 64;   // keys per tile
 constexpr int KPAD = 8;  // fp16 padding per K row in LDS
@@ -189,13 +191,15 @@ __device__ __forceinline__ void i4x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi
   hi = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, n, 0x04030402u)) - bias);
 }
 
-// fp16 copy of a scale when fp16(q) * fp16(s) rounds exactly like
-// fp16(float(q) * float(s)): s exact in fp16, normal, and |q * s| <= 65504
-// for |q| <= qmax. Otherwise 0 (callers take the fp32 route).
-__device__ __forceinline__ _Float16 exact_h(float s, float qmax) {
-  const _Float16 hs = (_Float16)s;
-  const bool ok = (float)hs == s && s >= 6.103515625e-05f && s * qmax <= 65504.0f;
-  return ok ? hs : (_Float16)0.0f;
+// True when fp16(q) * fp16(s) rounds exactly like fp16(float(q) * float(s))
+// for every integer |q| <= qmax: s exact in fp16, normal, and |q * s| <= 65504
+// (q * s is then exact in fp32, and the fp16 multiply rounds it once). bf16
+// and fp16 scales always fit fp16's significand, so only the range is tested.
+template <int SDT>
+__device__ __forceinline__ bool h_exact(float s, float qmax) {
+  const bool range = s >= 6.103515625e-05f && s * qmax <= 65504.0f;
+  if constexpr (SDT == SI_DT_F32) return range && (float)(_Float16)s == s;
+  return range;
 }
 
 // ---------------------------------------------------------------------------
@@ -214,12 +218,12 @@ __device__ __forceinline__ _Float16 exact_h(float s, float qmax) {
 //    tile ahead (slot lists two tiles ahead), K row-major and V transposed;
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: lane l holds scores of query
 //    l % 32 for 16 keys (lane l ^ 32 the other 16);
-//  * int8 K tiles keep the raw integers in LDS (exact in fp16) and apply the
-//    per-key scale to the score in fp32: exact arithmetic on the reference's
-//    float(q) * float(s) dequantization;
-//  * online softmax in the log2 domain; the running max is only raised when a
-//    score exceeds it by more than 2^8 (probabilities stay <= 256), so the
-//    output rescale is rare;
+//  * int8 and int4 K/V values q * s are rounded once to fp16 in the decode;
+//  * online softmax in the log2 domain: the score accumulators start at -m
+//    (the running max), so no subtraction follows the MFMAs; the running max
+//    is only raised when a score exceeds it by more than 2^8 (probabilities
+//    stay <= 256), so the output rescale is rare; the row sum adds the fp16
+//    probabilities with v_dot2_f32_f16;
 //  * O^T += V^T P^T reuses the score registers as the B operand (the k order
 //    of an MFMA only has to agree between A and B: V^T is read in the score
 //    accumulator's key order 8*(i/4) + 4*(l/32) + i%4).
@@ -244,7 +248,6 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   // Two tile buffers: tile t+1 is decoded into one while tile t is multiplied from the other.
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][BN][D + KPAD];
   __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D][VP];
-  __shared__ __attribute__((aligned(16))) float ksc[2][BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -284,7 +287,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   }
   const int n_ev = cnt[4];
   const int32_t* lh = lists + h * cap;
-  auto tile_valid = [&](int tt, int p) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
+  auto tile_valid = [&](int tt, int p) __attribute__((always_inline)) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
 
   // Decode-stage coordinates: keys 4*kg .. 4*kg+3 of the tile, dims d0 .. d0+DPT-1.
   const int kg = tid / C::DGN;
@@ -304,12 +307,12 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   // unconditional: indices past the phase's last tile are clamped to it (a
   // harmless re-read).
   int t_last = 0;  // last tile of the current phase
-  auto fetch_slots = [&](int tt) {
+  auto fetch_slots = [&](int tt) __attribute__((always_inline)) {
     tt = min(tt, t_last);
     sl = *reinterpret_cast<const int4*>(lh + (int64_t)tt * BN + 4 * kg);
   };
   // Raw loads of the tile's rows into registers (fp32 tiles are read at decode time).
-  auto fetch_data = [&](auto PC, int tt) {
+  auto fetch_data = [&](auto PC, int tt) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
     tt = min(tt, t_last);
     const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
@@ -351,9 +354,8 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   float l_run = 0.0f;
 
   // Decode tile tt (its rows are in rk / rv) into LDS buffer buf.
-  auto decode_tile = [&](auto PC, int tt, int buf) {
+  auto decode_tile = [&](auto PC, int tt, int buf) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
-    constexpr int p = P;
     const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
     {
       // The prefetched registers are first read here: nothing computed from
@@ -380,39 +382,23 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
             kw[i][x] = rk[i][x];
             vw[i][x] = rv[i][x];
           }
-      } else if constexpr (P == SI_PREC_INT8) {
+      } else if constexpr (P == SI_PREC_INT8 || P == SI_PREC_INT4) {
+        // Integer codes as exact fp16 pairs.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // K keeps the integer values (exact in fp16); the scale multiplies the score.
-          uint32_t unused;
-          if constexpr (DPT >= 4) {
+          if constexpr (P == SI_PREC_INT8) {
+            uint32_t unused;
+            if constexpr (DPT >= 4) {
 #pragma unroll
-            for (int x = 0; x < DPT / 4; ++x) {
-              i8x4_to_h(rk[i][x], kw[i][2 * x], kw[i][2 * x + 1]);
-              i8x4_to_h(rv[i][x], vw[i][2 * x], vw[i][2 * x + 1]);
+              for (int x = 0; x < DPT / 4; ++x) {
+                i8x4_to_h(rk[i][x], kw[i][2 * x], kw[i][2 * x + 1]);
+                i8x4_to_h(rv[i][x], vw[i][2 * x], vw[i][2 * x + 1]);
+              }
+            } else {
+              i8x4_to_h(rk[i][0], kw[i][0], unused);
+              i8x4_to_h(rv[i][0], vw[i][0], unused);
             }
-          } else {
-            i8x4_to_h(rk[i][0], kw[i][0], unused);
-            i8x4_to_h(rv[i][0], vw[i][0], unused);
-          }
-          // V: float(q) * float(s) rounded to fp16
-          const _Float16 hs = exact_h(sv[i], 128.0f);
-          if (hs != (_Float16)0.0f) {
-            const h2 s2 = {hs, hs};
-#pragma unroll
-            for (int x = 0; x < RW; ++x) vw[i][x] = as_u32(as_h2(vw[i][x]) * s2);
-          } else {
-#pragma unroll
-            for (int x = 0; x < RW; ++x) {
-              const h2 q = as_h2(vw[i][x]);
-              vw[i][x] = pack_h2((_Float16)((float)q[0] * sv[i]), (_Float16)((float)q[1] * sv[i]));
-            }
-          }
-        }
-      } else if constexpr (P == SI_PREC_INT4) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if constexpr (DPT >= 4) {
+          } else if constexpr (DPT >= 4) {
 #pragma unroll
             for (int x = 0; x < DPT / 4; ++x) {
               i4x4_to_h(rk[i][0] >> (16 * x), kw[i][2 * x], kw[i][2 * x + 1]);
@@ -423,23 +409,33 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
             kw[i][0] = pack_h2((_Float16)(float)((int)(kb >> 4) - 8), (_Float16)(float)((int)(kb & 0xfu) - 8));
             vw[i][0] = pack_h2((_Float16)(float)((int)(vb >> 4) - 8), (_Float16)(float)((int)(vb & 0xfu) - 8));
           }
-          // float(q) * float(s) rounded to fp16, for K and V
-          const _Float16 hk = exact_h(sk[i], 8.0f), hv = exact_h(sv[i], 8.0f);
-          if (hk != (_Float16)0.0f && hv != (_Float16)0.0f) {
-            const h2 k2 = {hk, hk}, v2 = {hv, hv};
+        }
+        // K and V values float(q) * float(s) rounded once to fp16: a packed fp16
+        // multiply when that rounds the same way for the whole wave (always, for
+        // scales of ordinary magnitude), else through fp32.
+        constexpr float qmax = P == SI_PREC_INT8 ? 128.0f : 8.0f;
+        bool fast = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fast = fast && h_exact<SDT>(sk[i], qmax) && h_exact<SDT>(sv[i], qmax);
+        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const h2 k2 = {(_Float16)sk[i], (_Float16)sk[i]}, v2 = {(_Float16)sv[i], (_Float16)sv[i]};
 #pragma unroll
             for (int x = 0; x < RW; ++x) {
               kw[i][x] = as_u32(as_h2(kw[i][x]) * k2);
               vw[i][x] = as_u32(as_h2(vw[i][x]) * v2);
             }
-          } else {
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int x = 0; x < RW; ++x) {
               const h2 a = as_h2(kw[i][x]), c = as_h2(vw[i][x]);
               kw[i][x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
               vw[i][x] = pack_h2((_Float16)((float)c[0] * sv[i]), (_Float16)((float)c[1] * sv[i]));
             }
-          }
         }
       } else {  // fp32 bucket rows, read here
         const int sl4[4] = {sl_data.x, sl_data.y, sl_data.z, sl_data.w};
@@ -476,10 +472,6 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
           *reinterpret_cast<uint32_t*>(&Ks[buf][4 * kg + i][d0]) = kw[i][0];
         }
       }
-      if (dg == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ksc[buf][4 * kg + i] = p == SI_PREC_INT8 ? sk[i] : 1.0f;
-      }
       // V^T rows d0 + e hold keys 4*kg .. 4*kg+3 (8 bytes): transpose the pair words.
 #pragma unroll
       for (int x = 0; x < RW; ++x) {
@@ -494,19 +486,22 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   };
 
   // S^T = K Q^T, online softmax and O^T += V^T P^T for tile tt in buffer buf.
-  auto compute_tile = [&](auto PC, int tt, int buf) {
+  auto compute_tile = [&](auto PC, int tt, int buf) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
     const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
-    // ---- S^T = K Q^T for the tile's 64 keys ----
+    // ---- S^T = K Q^T - m for the tile's 64 keys ----
+    // The accumulators start at -m_run (0 before the first tile), so the MFMAs
+    // return the scores already shifted by the running max.
     // K fragments of k-step ks+1 are read while the MFMAs of k-step ks run.
+    const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
     v16f sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) sacc[kb][r] = c0;
     {
       v8h ka[2][2];
-      auto load_k = [&](int ks, v8h* a) {
+      auto load_k = [&](int ks, v8h* a) __attribute__((always_inline)) {
         a[0] = *reinterpret_cast<const v8h*>(&Ks[buf][col][ks * 16 + 8 * grp]);
         a[1] = *reinterpret_cast<const v8h*>(&Ks[buf][32 + col][ks * 16 + 8 * grp]);
       };
@@ -524,19 +519,6 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     }
 
     // ---- online softmax (log2 domain; Q carries sm_scale * log2(e)) ----
-    if constexpr (P == SI_PREC_INT8) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 f = *reinterpret_cast<const float4*>(&ksc[buf][kb * 32 + 8 * q4 + 4 * grp]);
-          sacc[kb][4 * q4 + 0] *= f.x;
-          sacc[kb][4 * q4 + 1] *= f.y;
-          sacc[kb][4 * q4 + 2] *= f.z;
-          sacc[kb][4 * q4 + 3] *= f.w;
-        }
-      }
-    }
     if (nv < BN) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -549,64 +531,72 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], sacc[kb][r]);
+    // Shifted tile max; the running max is raised only when a score exceeds it
+    // by more than 8 (a factor 2^8), and always at the first tile.
     float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const bool raise = tmax > m_run + 8.0f;
+    const bool raise = m_run == -INFINITY || tmax > 8.0f;
     if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-      const float m_new = raise ? tmax : m_run;
+      const float m_new = raise ? tmax - c0 : m_run;
       const float alpha = exp2f(m_run - m_new);
+      const float delta = m_new + c0;  // tmax when raised, else 0
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DB; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] -= delta;
       m_run = m_new;
     }
-    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // P = 2^(s - m) as fp16 pairs (the B operand of the P.V MFMAs); the row sum
+    // adds the same fp16 values in fp32 (v_dot2_f32_f16 with {1, 1}).
+    uint32_t pw[16];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int j = 0; j < 8; ++j) {
         // v_exp_f32: arguments are <= 8 here; results below 2^-126 flush to 0
-        const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_run);
-        sacc[kb][r] = pr;
-        ps[r & 3] += pr;
+        const h2 pp = {(_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j]),
+                       (_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j + 1])};
+        pw[8 * kb + j] = as_u32(pp);
       }
-    }
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int w = 0; w < 16; ++w) ps[w & 3] = __builtin_amdgcn_fdot2(as_h2(pw[w]), ones, ps[w & 3], false);
     const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
     l_run += psum + __shfl_xor(psum, 32, 64);
 
     // ---- O^T += V^T P^T over four 16-key chunks ----
-    // V^T fragments of chunk c+1 are read while the MFMAs of chunk c run.
     {
-      v8h va[2][DB];
-      auto load_v = [&](int c, v8h* a) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const _Float16* vrow = &Vt[buf][db * 32 + col][c * 16 + 4 * grp];
-          const v4h lo = *reinterpret_cast<const v4h*>(vrow);
-          const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
-          a[db] = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+      // V^T fragments stream two (chunk, row block) steps ahead of their MFMA.
+      auto load_v = [&](int i) __attribute__((always_inline)) {
+        const int c = i / DB, db = i % DB;
+        const _Float16* vrow = &Vt[buf][db * 32 + col][c * 16 + 4 * grp];
+        const v4h lo = *reinterpret_cast<const v4h*>(vrow);
+        const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
+        return v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       };
-      load_v(0, va[0]);
+      constexpr int NV = 4 * DB;
+      v8h va[3];
+      va[0] = load_v(0);
+      va[1] = load_v(1);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (c + 1 < 4) load_v(c + 1, va[(c + 1) & 1]);
-        const int kb = c >> 1;
-        const int hc = c & 1;
-        v8h pb;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pb[i] = (_Float16)sacc[kb][8 * hc + i];
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c & 1][db], pb, o[db], 0, 0, 0);
+      for (int i = 0; i < NV; ++i) {
+        if (i + 2 < NV) va[(i + 2) % 3] = load_v(i + 2);
+        const int c = i / DB, db = i % DB;
+        const int base = 4 * c;  // keys 16c .. 16c+15 of the lane's score order
+        const v4i pi = {(int)pw[base], (int)pw[base + 1], (int)pw[base + 2], (int)pw[base + 3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[i % 3], __builtin_bit_cast(v8h, pi), o[db], 0, 0, 0);
       }
     }
   };
 
   int buf = 0;
-  auto run_phase = [&](auto PC) {
+  auto run_phase = [&](auto PC) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
     const int t0 = tstart[P], t1 = tstart[P + 1];
     if (t0 >= t1) return;
