@@ -20,6 +20,8 @@
 // fp32 online softmax; fp16 entries of the cache are exact in fp16, int8/int4
 // values q*s are rounded once to fp16, and P is rounded to fp16 for the P.V
 // MFMAs (its row sum adds the same fp16 values).
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "si_kv_common.h"
@@ -235,7 +237,9 @@ struct OutStrides {
   int64_t b, h, s;
 };
 
-template <int D, int SDT, int QDT>
+// O32: every bucket and scale buffer is below 2^31 bytes, so row addresses are
+// 32-bit byte offsets from the (uniform) buffer base.
+template <int D, int SDT, int QDT, bool O32>
 __global__ __launch_bounds__(512) void attn_packed_fwd(
     const uint16_t* __restrict__ Q, int64_t B, int64_t H, int64_t Sq, int64_t cap,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ lists, Buckets bk, int64_t g,
@@ -311,6 +315,16 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     tt = min(tt, t_last);
     sl = *reinterpret_cast<const int4*>(lh + (int64_t)tt * BN + 4 * kg);
   };
+  // Byte offset of a slot's row = slot * stride + this thread's constant part.
+  constexpr uint32_t SS = SDT == SI_DT_F32 ? 4 : 2;  // scale bytes
+  const uint32_t st16 = (uint32_t)(2 * B * D), c16 = (uint32_t)(2 * (b * D + d0));
+  const uint32_t st8 = (uint32_t)(B * D), c8 = (uint32_t)(b * D + d0);
+  const uint32_t st8s = (uint32_t)(B * SS), c8s = (uint32_t)(b * SS);
+  const uint32_t st4 = (uint32_t)(B * D / 2), c4 = (uint32_t)((b * D + d0) / 2);
+  const uint32_t st4s = (uint32_t)(B * ngrp * SS), c4s = (uint32_t)((b * ngrp + my_grp) * SS);
+  auto at = [&](int j, uint32_t off) __attribute__((always_inline)) {
+    return reinterpret_cast<const char*>(bk.p[j]) + off;
+  };
   // Raw loads of the tile's rows into registers (fp32 tiles are read at decode time).
   auto fetch_data = [&](auto PC, int tt) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
@@ -324,6 +338,24 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
       // Keys past the tile's valid count read row 0 of the same (non-empty)
       // bucket: their scores are masked to -inf, so they contribute nothing.
       const int sli = 4 * kg + i < nv ? sl4[i] : 0;
+      if constexpr (O32) {
+        const uint32_t us = (uint32_t)sli;
+        if constexpr (P == SI_PREC_FP16) {
+          load_raw<2 * DPT>(at(4, us * st16 + c16), rk[i]);
+          load_raw<2 * DPT>(at(5, us * st16 + c16), rv[i]);
+        } else if constexpr (P == SI_PREC_INT8) {
+          load_raw<DPT>(at(8, us * st8 + c8), rk[i]);
+          load_raw<DPT>(at(9, us * st8 + c8), rv[i]);
+          load_raw<SS>(at(10, us * st8s + c8s), &skb[i]);
+          load_raw<SS>(at(11, us * st8s + c8s), &svb[i]);
+        } else if constexpr (P == SI_PREC_INT4) {
+          load_raw<DPT / 2>(at(12, us * st4 + c4), rk[i]);
+          load_raw<DPT / 2>(at(13, us * st4 + c4), rv[i]);
+          load_raw<SS>(at(14, us * st4s + c4s), &skb[i]);
+          load_raw<SS>(at(15, us * st4s + c4s), &svb[i]);
+        }
+        continue;
+      }
       const int64_t row = (int64_t)sli * B + b;
       if constexpr (P == SI_PREC_FP16) {
         load_raw<2 * DPT>(reinterpret_cast<const uint16_t*>(bk.p[4]) + row * D + d0, rk[i]);
@@ -662,25 +694,42 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   }
 }
 
+template <int D, int QDT, bool O32>
+void launch_attn_o(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t B, int64_t H,
+                   int64_t Sq, int64_t cap, const int32_t* counts, const int32_t* lists,
+                   const Buckets& bk, int64_t g, float scale_log2, void* out, int odt,
+                   const OutStrides& os) {
+  constexpr int NT = 64 * AttnCfg<D>::NW;
+  switch (sdt) {
+    case SI_DT_F32:
+      attn_packed_fwd<D, SI_DT_F32, QDT, O32><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
+                                                                   bk, g, scale_log2, out, odt, os);
+      break;
+    case SI_DT_F16:
+      attn_packed_fwd<D, SI_DT_F16, QDT, O32><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
+                                                                   bk, g, scale_log2, out, odt, os);
+      break;
+    default:
+      attn_packed_fwd<D, SI_DT_BF16, QDT, O32><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
+                                                                    bk, g, scale_log2, out, odt, os);
+  }
+}
+
+// A bucket holds at most n_max = S_kv * H entries; fp32 rows (B * D * 4 bytes)
+// bound the byte offsets of every bucket and scale buffer.
 template <int D, int QDT>
 void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t B, int64_t H,
                  int64_t Sq, int64_t cap, const int32_t* counts, const int32_t* lists,
                  const Buckets& bk, int64_t g, float scale_log2, void* out, int odt,
-                 const OutStrides& os) {
-  constexpr int NT = 64 * AttnCfg<D>::NW;
-  switch (sdt) {
-    case SI_DT_F32:
-      attn_packed_fwd<D, SI_DT_F32, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
-                                                              g, scale_log2, out, odt, os);
-      break;
-    case SI_DT_F16:
-      attn_packed_fwd<D, SI_DT_F16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists, bk,
-                                                              g, scale_log2, out, odt, os);
-      break;
-    default:
-      attn_packed_fwd<D, SI_DT_BF16, QDT><<<grid, NT, 0, st>>>(q, B, H, Sq, cap, counts, lists,
-                                                               bk, g, scale_log2, out, odt, os);
-  }
+                 const OutStrides& os, int64_t n_max) {
+  // SI_ATTN_OFFSET64 (any value) selects the 64-bit addressing at every size, so tests can
+  // compare the two paths on small caches.
+  if (n_max * B * D * 4 < ((int64_t)1 << 31) && getenv("SI_ATTN_OFFSET64") == nullptr)
+    launch_attn_o<D, QDT, true>(sdt, grid, st, q, B, H, Sq, cap, counts, lists, bk, g, scale_log2,
+                                out, odt, os);
+  else
+    launch_attn_o<D, QDT, false>(sdt, grid, st, q, B, H, Sq, cap, counts, lists, bk, g, scale_log2,
+                                 out, odt, os);
 }
 
 }  // namespace
@@ -737,17 +786,17 @@ int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int6
   if (D == 128) {
     if (q_dtype == SI_DT_BF16)
       launch_attn<128, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                   group, scale_log2, out, out_dtype, os);
+                                   group, scale_log2, out, out_dtype, os, S_kv * H);
     else
       launch_attn<128, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                  group, scale_log2, out, out_dtype, os);
+                                  group, scale_log2, out, out_dtype, os, S_kv * H);
   } else {
     if (q_dtype == SI_DT_BF16)
       launch_attn<64, SI_DT_BF16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                  group, scale_log2, out, out_dtype, os);
+                                  group, scale_log2, out, out_dtype, os, S_kv * H);
     else
       launch_attn<64, SI_DT_F16>(scale_dtype, grid, st, qp, B, H, S_q, cap, counts, lists, bk,
-                                 group, scale_log2, out, out_dtype, os);
+                                 group, scale_log2, out, out_dtype, os, S_kv * H);
   }
   return check_launch("si_attn_packed_fwd");
 }

@@ -143,3 +143,26 @@ def test_attention_entry_points_agree(dev, D):
         assert torch.equal(got, out)
     again = PackedKVCache.pack((k * 2).to(dev), v.to(dev), None, plan=plan)["packed_kv"]
     assert again.attention_lists() is cache.attention_lists()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_offset_widths_agree(dev, D, monkeypatch):
+    """Caches below 2^31 bytes address bucket rows with 32-bit offsets; larger
+    ones with 64-bit addresses. SI_ATTN_OFFSET64 selects the 64-bit path at any
+    size: both give the same bits, and both match the oracle."""
+    B, H, S = 2, 3, 300
+    k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=D + 7, outlier_frac=0.02)
+    codes = mixed_codes(S, H, seed=D + 7, probs=(1, 1, 2, 1), sink=4, evicted=0.05)
+    cache = _pack(k, v, codes, dev)
+    g = torch.Generator().manual_seed(D)
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
+    narrow = packed_attention(q, cache)
+    monkeypatch.setenv("SI_ATTN_OFFSET64", "1")
+    wide = packed_attention(q, cache)
+    monkeypatch.delenv("SI_ATTN_OFFSET64")
+    assert torch.equal(narrow, wide)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
+    ref = O.attention(q.float().cpu().numpy().reshape(B * H, S, D), rk.reshape(B * H, S, D),
+                      rv.reshape(B * H, S, D)).reshape(B, H, S, D)
+    assert _rel_l2(wide.float().cpu(), ref) <= TOL
