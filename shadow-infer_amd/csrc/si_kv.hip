@@ -1175,7 +1175,14 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(
 // rows, no divergence between precisions.
 // ---------------------------------------------------------------------------
 
-constexpr int kListRows = 64;
+#ifndef SI_LIST_ROWS
+#define SI_LIST_ROWS 128
+#endif
+constexpr int kListRows = SI_LIST_ROWS;
+
+// The unit indices of one block's rows need 64 bits only when kListRows fp32
+// rows of B * D values reach 2^32 bytes.
+inline bool list_rows_wide(int64_t B, int64_t D) { return B * D * 4 * kListRows >= ((int64_t)1 << 32); }
 
 struct CopyLists {
   const int64_t* flat[4];  // destination slot order: h*S + t
@@ -1183,18 +1190,20 @@ struct CopyLists {
   int64_t blk_end[4];
 };
 
-template <int U>
+// WIDE: 64-bit unit indices (rows * row_bytes may exceed 2^32).
+template <int U, bool WIDE>
 __device__ __forceinline__ void copy_units(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
                                            int64_t row_bytes, int64_t s0, int rows,
                                            const int64_t* srcs) {
   typedef typename std::conditional<U == 16, uint4,
           typename std::conditional<U == 4, uint32_t,
           typename std::conditional<U == 2, uint16_t, uint8_t>::type>::type>::type T;
-  const int64_t cpr = row_bytes / U;
-  const int64_t total = rows * cpr;
-  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
-    const int64_t r = i / cpr;
-    const int64_t c = i - r * cpr;
+  typedef typename std::conditional<WIDE, int64_t, unsigned>::type I;
+  const I cpr = (I)(row_bytes / U);
+  const I total = (I)rows * cpr;
+  for (I i = threadIdx.x; i < total; i += blockDim.x) {
+    const I r = i / cpr;
+    const I c = i - r * cpr;
     const int64_t ss = srcs[r];
     if (ss < 0) continue;
     *reinterpret_cast<T*>(dst + (s0 + r) * row_bytes + c * U) =
@@ -1203,6 +1212,7 @@ __device__ __forceinline__ void copy_units(uint8_t* __restrict__ dst, const uint
 }
 
 // Rows s0 .. s0+rows-1 of dst <- rows srcs[r] of src (skipped where srcs[r] < 0).
+template <bool WIDE>
 __device__ __forceinline__ void copy_rows(void* dst, const void* src, int64_t row_bytes, int64_t s0,
                                           int rows, const int64_t* srcs) {
   if (dst == nullptr || src == nullptr || row_bytes == 0) return;
@@ -1210,10 +1220,10 @@ __device__ __forceinline__ void copy_rows(void* dst, const void* src, int64_t ro
   const uint8_t* sp = reinterpret_cast<const uint8_t*>(src);
   const uintptr_t mis = reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(sp) |
                         (uintptr_t)row_bytes;
-  if ((mis & 15) == 0) copy_units<16>(d, sp, row_bytes, s0, rows, srcs);
-  else if ((mis & 3) == 0) copy_units<4>(d, sp, row_bytes, s0, rows, srcs);
-  else if ((mis & 1) == 0) copy_units<2>(d, sp, row_bytes, s0, rows, srcs);
-  else copy_units<1>(d, sp, row_bytes, s0, rows, srcs);
+  if ((mis & 15) == 0) copy_units<16, WIDE>(d, sp, row_bytes, s0, rows, srcs);
+  else if ((mis & 3) == 0) copy_units<4, WIDE>(d, sp, row_bytes, s0, rows, srcs);
+  else if ((mis & 1) == 0) copy_units<2, WIDE>(d, sp, row_bytes, s0, rows, srcs);
+  else copy_units<1, WIDE>(d, sp, row_bytes, s0, rows, srcs);
 }
 
 // REUSE: destination = current cache, source = previous cache (same H, so the
@@ -1221,7 +1231,7 @@ __device__ __forceinline__ void copy_rows(void* dst, const void* src, int64_t ro
 // and the previous code equals the row's precision (apply_reuse_mask,
 // packed_kv_cache.py:791-852). Otherwise (compaction, :698-737): every row is
 // copied from src_slot[e] of the old buckets.
-template <bool REUSE>
+template <bool REUSE, bool WIDE>
 __global__ __launch_bounds__(256) void kv_copy_lists(CopyLists L, Buckets dst, Buckets src,
                                                      const int8_t* __restrict__ src_code,
                                                      const int32_t* __restrict__ src_slot,
@@ -1260,9 +1270,9 @@ __global__ __launch_bounds__(256) void kv_copy_lists(CopyLists L, Buckets dst, B
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    copy_rows(dst.p[4 * p + j], src.p[4 * p + j], geo.data_bytes[p], s0, rows, srcs);
+    copy_rows<WIDE>(dst.p[4 * p + j], src.p[4 * p + j], geo.data_bytes[p], s0, rows, srcs);
     if (geo.scale_bytes[p] > 0)
-      copy_rows(dst.p[4 * p + 2 + j], src.p[4 * p + 2 + j], geo.scale_bytes[p], s0, rows, srcs);
+      copy_rows<WIDE>(dst.p[4 * p + 2 + j], src.p[4 * p + 2 + j], geo.scale_bytes[p], s0, rows, srcs);
   }
   if (REUSE && stats != nullptr && threadIdx.x == 0 && (cnt[0] | cnt[1])) {
     atomicAdd(stats, (unsigned long long)cnt[0]);
@@ -1708,9 +1718,15 @@ extern "C" int si_kv_reuse_flat(const int64_t* const* cur_flat, const int64_t* c
     SI_CHECK_ARG(L.n[p] == 0 || L.flat[p] != nullptr, "si_kv_reuse_flat: NULL list %d", p);
   if (blocks == 0) return SI_OK;
   SI_CHECK_ARG(blocks < ((int64_t)1 << 31), "si_kv_reuse_flat: too many blocks");
-  kv_copy_lists<true><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
-      L, dst, to_buckets(prev_buckets), prev_code, prev_slot, mask, S, H, S_prev,
-      make_geom(B, D, group, scale_dtype), reinterpret_cast<unsigned long long*>(stats));
+  const RowGeom geo = make_geom(B, D, group, scale_dtype);
+  if (list_rows_wide(B, D))
+    kv_copy_lists<true, true><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+        L, dst, to_buckets(prev_buckets), prev_code, prev_slot, mask, S, H, S_prev, geo,
+        reinterpret_cast<unsigned long long*>(stats));
+  else
+    kv_copy_lists<true, false><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+        L, dst, to_buckets(prev_buckets), prev_code, prev_slot, mask, S, H, S_prev, geo,
+        reinterpret_cast<unsigned long long*>(stats));
   return check_launch("si_kv_reuse_flat");
 }
 
@@ -1733,9 +1749,13 @@ extern "C" int si_kv_compact_flat(const int32_t* old_slot, const void* const* ol
     SI_CHECK_ARG(L.n[p] == 0 || L.flat[p] != nullptr, "si_kv_compact_flat: NULL list %d", p);
   if (blocks == 0) return SI_OK;
   SI_CHECK_ARG(blocks < ((int64_t)1 << 31), "si_kv_compact_flat: too many blocks");
-  kv_copy_lists<false><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
-      L, dst, to_buckets(old_buckets), nullptr, old_slot, nullptr, S, H, S,
-      make_geom(B, D, group, scale_dtype), nullptr);
+  const RowGeom geo = make_geom(B, D, group, scale_dtype);
+  if (list_rows_wide(B, D))
+    kv_copy_lists<false, true><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+        L, dst, to_buckets(old_buckets), nullptr, old_slot, nullptr, S, H, S, geo, nullptr);
+  else
+    kv_copy_lists<false, false><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+        L, dst, to_buckets(old_buckets), nullptr, old_slot, nullptr, S, H, S, geo, nullptr);
   return check_launch("si_kv_compact_flat");
 }
 
