@@ -544,9 +544,10 @@ def bench_step(torch, dev, steps=8, warmup=2, gen_steps=64):
     return res
 
 
-def cpu_baseline(layers: int = 4):
-    """The oracle (C + numpy, one thread) on ``layers`` of the same layers:
-    pack + unpack, algorithmic bytes / wall time."""
+def cpu_baseline(layers: int = 16):
+    """The oracle (C + numpy, one thread) on ``layers`` of the 32 layers (each
+    layer's own precision codes, one seeded K/V): pack + unpack, algorithmic
+    bytes / wall time of the oracle calls (about 10 s)."""
     import numpy as np
     import torch
     sys.path.insert(0, ROOT)
@@ -555,11 +556,11 @@ def cpu_baseline(layers: int = 4):
     O.build()
     total_bytes, total_s = 0, 0.0
     gen = torch.Generator().manual_seed(99)
+    k = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
+    kn = k.view(torch.int16).numpy().view(np.uint16)
+    vn = v.view(torch.int16).numpy().view(np.uint16)
     for layer in range(layers):
-        k = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
-        v = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
-        kn = k.view(torch.int16).numpy().view(np.uint16)
-        vn = v.view(torch.int16).numpy().view(np.uint16)
         codes = make_codes(1000 + layer)
         t0 = time.perf_counter()
         cache = O.kv_pack(kn, vn, O.BF16, codes, GROUP)

@@ -194,14 +194,18 @@ __device__ __forceinline__ void i4x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi
 }
 
 // True when fp16(q) * fp16(s) rounds exactly like fp16(float(q) * float(s))
-// for every integer |q| <= qmax: s exact in fp16, normal, and |q * s| <= 65504
-// (q * s is then exact in fp32, and the fp16 multiply rounds it once). bf16
-// and fp16 scales always fit fp16's significand, so only the range is tested.
-template <int SDT>
-__device__ __forceinline__ bool h_exact(float s, float qmax) {
-  const bool range = s >= 6.103515625e-05f && s * qmax <= 65504.0f;
-  if constexpr (SDT == SI_DT_F32) return range && (float)(_Float16)s == s;
-  return range;
+// for every integer |q| <= qmax (128 for int8, 8 for int4): s exact in fp16,
+// normal, and |q * s| <= 65504 (q * s is then exact in fp32, and the fp16
+// multiply rounds it once). bf16 and fp16 scales always fit fp16's
+// significand, so their test is a range test on the raw bits: 2^-14 <= s and
+// s <= 65504 / qmax (bf16 0x3880 .. 0x43FF / 0x45FF, fp16 0x0400 .. 0x5FFF /
+// 0x6FFF), which also rejects negative scales.
+template <int SDT, bool I8>
+__device__ __forceinline__ bool h_exact(uint32_t bits, float s) {
+  if constexpr (SDT == SI_DT_BF16) return bits - 0x3880u <= (I8 ? 0x43FFu : 0x45FFu) - 0x3880u;
+  if constexpr (SDT == SI_DT_F16) return bits - 0x0400u <= (I8 ? 0x5FFFu : 0x6FFFu) - 0x0400u;
+  const float qmax = I8 ? 128.0f : 8.0f;
+  return s >= 6.103515625e-05f && s * qmax <= 65504.0f && (float)(_Float16)s == s;
 }
 
 // ---------------------------------------------------------------------------
@@ -445,11 +449,12 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         // K and V values float(q) * float(s) rounded once to fp16: a packed fp16
         // multiply when that rounds the same way for the whole wave (always, for
         // scales of ordinary magnitude), else through fp32.
-        constexpr float qmax = P == SI_PREC_INT8 ? 128.0f : 8.0f;
-        bool fast = true;
+        int fast = 1;  // int, not bool: '&' keeps the eight tests branch-free
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fast = fast && h_exact<SDT>(sk[i], qmax) && h_exact<SDT>(sv[i], qmax);
-        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+        for (int i = 0; i < 4; ++i)
+          fast &= (int)h_exact<SDT, P == SI_PREC_INT8>(skb[i], sk[i]) &
+                  (int)h_exact<SDT, P == SI_PREC_INT8>(svb[i], sv[i]);
+        if (__builtin_amdgcn_ballot_w64(fast == 0) == 0) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const h2 k2 = {(_Float16)sk[i], (_Float16)sk[i]}, v2 = {(_Float16)sv[i], (_Float16)sv[i]};

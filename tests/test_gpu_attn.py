@@ -166,3 +166,32 @@ def test_attention_offset_widths_agree(dev, D, monkeypatch):
     ref = O.attention(q.float().cpu().numpy().reshape(B * H, S, D), rk.reshape(B * H, S, D),
                       rv.reshape(B * H, S, D)).reshape(B, H, S, D)
     assert _rel_l2(wide.float().cpu(), ref) <= TOL
+
+
+@pytest.mark.gpu
+def test_attention_extreme_scales(dev):
+    """Rows whose int8/int4 scales leave the range where a packed fp16 multiply
+    rounds like the fp32 product (scales below 2^-14, or q * s near the fp16
+    limit) take the decode's fp32 route; the result still matches the oracle."""
+    B, H, S, D = 1, 2, 256, 128
+    k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=5)
+    k, v = k.float(), v.float()
+    k[:, :, 10:20] *= 1e-4                      # int8 scale ~3e-6, int4 ~5e-5: below 2^-14
+    v[:, :, 10:20] *= 1e-4
+    big = v[:, :, 30:40]
+    v[:, :, 30:40] = big / big.abs().amax(dim=-1, keepdim=True) * 65000.0  # s*128 > 65504
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    codes = mixed_codes(S, H, seed=5, probs=(1, 1, 2, 1), sink=4)
+    codes[10:20, 0] = 2
+    codes[10:20, 1] = 3
+    codes[30:40, 0] = 2
+    codes[30:40, 1] = 3
+    cache = _pack(k, v, codes, dev)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    out = packed_attention(q.to(dev), cache)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
+    assert np.isfinite(rv).all()
+    ref = O.attention(q.float().numpy().reshape(B * H, S, D), rk.reshape(B * H, S, D),
+                      rv.reshape(B * H, S, D)).reshape(B, H, S, D)
+    assert _rel_l2(out.float().cpu(), ref) <= TOL
