@@ -573,6 +573,33 @@ def cpu_baseline(layers: int = 16):
             "seconds": total_s}
 
 
+def cpu_gemm_baseline(ms=(16, 64)):
+    """The oracle's INT8Linear forward (C, one thread: activation quant, int8 x
+    int8 -> int32 GEMM, epilogue) on the 4096 x 11008 FFN shape for the given
+    M, on the host: microseconds and TOPS per M."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+
+    O.build()
+    K, N = 4096, 11008
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((K, N), dtype=np.float32) * 0.02
+    sw = (np.abs(w).max(axis=0) / 127).astype(np.float32)
+    qw = np.clip(np.rint(w / sw), -127, 127).astype(np.int8)  # [K, N], the reference's layout
+    out = {}
+    for M in ms:
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        xb = (x.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated draw)
+        t0 = time.perf_counter()
+        O.int8_linear_forward(xb, O.BF16, qw, sw)
+        dt = time.perf_counter() - t0
+        out[str(M)] = {"us": dt * 1e6, "tops": 2.0 * M * K * N / dt / 1e12}
+    return {"kind": "port", "cores": 1,
+            "sample": "oracle INT8Linear forward (C, 1 thread) on 4096 x 11008, M in "
+                      + ", ".join(str(m) for m in ms), **out}
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of ``kernel`` from the committed counter summary
     (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the factor a plain
@@ -648,10 +675,15 @@ def main():
         log("denoising step")
         step = bench_step(torch, dev)
     cpu = None
+    gemm_cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle)")
         cpu = cpu_baseline()
         log(f"cpu {cpu['value']:.3f} GB/s in {cpu['seconds']:.1f} s")
+        if gemm is not None:
+            gemm_cpu = cpu_gemm_baseline()
+            log("cpu gemm " + ", ".join(f"M={m} {gemm_cpu[m]['us'] / 1e3:.0f} ms"
+                                         for m in ("16", "64")))
 
     dom = "unpack" if kv["unpack_us"] >= kv["pack_us"] else "pack"
     achieved = kv[f"{dom}_gbs"]
@@ -692,6 +724,10 @@ def main():
     if gemm is not None:
         line["int8_gemm"] = {"shape": "M x 4096 x 11008", "peak_tops": INT8_PEAK_TOPS,
                              **{m: {k: round(v, 4) for k, v in r.items()} for m, r in gemm.items()}}
+        if gemm_cpu is not None:
+            line["int8_gemm"]["cpu_baseline"] = {
+                k: ({kk: round(vv, 4) for kk, vv in v.items()} if isinstance(v, dict) else v)
+                for k, v in gemm_cpu.items()}
     if attn is not None:
         line["packed_attention"] = {"shape": "B=1, H=32, D=128, S_q=S_kv", "peak_tflops": FP16_PEAK_TFLOPS,
                                     **{s: {k: round(v, 4) for k, v in r.items()} for s, r in attn.items()}}
