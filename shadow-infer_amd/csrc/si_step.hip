@@ -238,7 +238,16 @@ __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu,
         load8<DT>(gu, m * 2 * F + F + (int64_t)c * 8, u);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float sg = round_to(g[e] / (1.0f + expf(-g[e])), DT);
+          float sg;
+          if constexpr (DT == SI_DT_F32) {
+            sg = g[e] / (1.0f + expf(-g[e]));
+          } else {
+            // g / (1 + exp(-g)) with v_exp_f32 and v_rcp_f32: a few fp32 ulps from
+            // the correctly rounded quotient, below half a bf16/fp16 ulp, before
+            // the rounding to T
+            const float ex = __builtin_amdgcn_exp2f(-g[e] * 1.44269504088896341f);
+            sg = round_to(g[e] * __builtin_amdgcn_rcpf(1.0f + ex), DT);
+          }
           v[r][e] = round_to(sg * u[e], DT);
         }
         if (h != nullptr) store8<DT>(h, m * F + (int64_t)c * 8, v[r]);
