@@ -22,6 +22,7 @@
 // MFMAs (its row sum adds the same fp16 values).
 #include <stdlib.h>
 
+
 #include <type_traits>
 
 #include "si_kv_common.h"
@@ -543,6 +544,10 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         a[1] = *reinterpret_cast<const v8h*>(&Ks[buf][32 + col][ks * 16 + 8 * grp]);
       };
       load_k(0, ka[0]);
+      // Raised wave priority from the first QK^T MFMA to the last P.V MFMA: when
+      // both waves of a SIMD have instructions ready, the one feeding the
+      // matrix core issues first (S=8192: 1.42 -> 1.38 ms).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) load_k(ks + 1, ka[(ks + 1) & 1]);
@@ -629,6 +634,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         const v4i pi = {(int)pw[base], (int)pw[base + 1], (int)pw[base + 2], (int)pw[base + 3]};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[i % 3], __builtin_bit_cast(v8h, pi), o[db], 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
   };
 
