@@ -803,7 +803,9 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             // eight waves on a 128x128 tile (4x2 and 2x4 wave grids)
             K_DMA8_128x128_42 = 30, K_DMA8_128x128_24 = 31,
             // weight streaming with 32 / 16 output columns per block
-            K_STREAM_N32 = 32, K_STREAM_N16 = 33, K_STREAM_N32_W8 = 34, K_STREAM_N16_W8 = 35 };
+            K_STREAM_N32 = 32, K_STREAM_N16 = 33, K_STREAM_N32_W8 = 34, K_STREAM_N16_W8 = 35,
+            // 64-row tiles for 33 <= M <= 64 (no rows of padding in the A tile)
+            K_DMA_64x64 = 38, K_DMA_64x128 = 39 };
 
 struct Plan {
   int kind;
@@ -832,13 +834,45 @@ int forced_splits() {
   return splits;
 }
 
+// Tile and split-K choice for 16 < M <= 128 with K % 128 == 0, where each CU
+// holds at most one block and a block's time is set by how fast its CU can
+// pull A and B rows out of L2 (about 63 GB/s per CU with 4 waves), plus a
+// fixed 6.7 us per wave of blocks; split K adds the int32 partial round trip
+// through gemm_finalize (2 us + bytes at ~4 TB/s). Fitted on 4096 x 11008,
+// 11008 x 4096 and 4096 x 22016 at M = 24..192, where it reproduces the
+// measured times within ~10%. Returns the kind and sets *splits.
+int choose_fill(int64_t M, int64_t N, int64_t K, int* splits) {
+  struct Cand { int kind, bm, bn; };
+  const Cand cands[3] = {{K_DMA_64x64, 64, 64}, {K_DMA_64x128, 64, 128},
+                         {K_DMA8_128x128_24, 128, 128}};
+  const int64_t kt = K / 128;
+  double best = 0.0;
+  int kind = K_DMA8_128x128_24;
+  *splits = 1;
+  for (const Cand& c : cands) {
+    for (int s = 1; s <= 8; s *= 2) {
+      if (s > 1 && kt / s < 16) break;  // shorter K loops lose more than the model says
+      const int64_t per = ceil_div(kt, s);
+      const int64_t blocks = ceil_div(M, c.bm) * ceil_div(N, c.bn) * ceil_div(kt, per);
+      double t = (double)ceil_div(blocks, 256) *
+                 (6.7 + 15.9e-6 * (double)(c.bm + c.bn) * (double)(per * 128));
+      if (s > 1) t += 2.0 + (double)(s + 1) * (double)M * (double)N * 4.0 / 4.0e6;
+      if (best == 0.0 || t < best * (1.0 - 1e-9)) { best = t; kind = c.kind; *splits = s; }
+    }
+  }
+  return kind;
+}
+
 Plan choose(int64_t M, int64_t N, int64_t K) {
   Plan p{K_SCALAR, 0, 1, (int)K, 0, 0, 0};
   const bool big = M >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 31);
   if (K % 16 != 0 || M == 0 || N == 0 || big) return p;
   int kind;
+  int fill_splits = 0;
   if (forced_kind() >= 0) {
     kind = forced_kind();
+  } else if (M > 16 && M <= 128 && K % 128 == 0) {
+    kind = choose_fill(M, N, K, &fill_splits);
   } else if (M <= 32 && K % 64 == 0) {
     // Weight streaming; the column width per block sets how many CUs stream.
     // M = 16: N = 11008 -> 64 columns (172 blocks, 12 us); N = 4096 -> 16
@@ -849,7 +883,7 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (K % 128 == 0) {
     // One tile per CU per wave of tiles. Estimated time = waves of 256 tiles
     // x (tile area / the tile's measured speed relative to 256x256); the
-    // smallest wins. 4096 x 11008: M = 64..256 -> 128x128 (M = 256: 21.7 us),
+    // smallest wins. 4096 x 11008: M = 129..256 -> 128x128 (M = 256: 21.7 us),
     // M = 384..512 -> 256x128, M = 640 -> 128x128, M = 1024 -> 256x192;
     // 2048 x 22016 x 4096 -> 256x256; 2048 x 4096 x 11008 -> 256x128.
     struct Cand { int kind, bm, bn; double speed; };
@@ -910,6 +944,8 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     case K_DMA8_128x256: p.bm = 128; p.bn = 256; p.bk = 64; break;
     case K_DMA8_128x128_42: p.bm = 128; p.bn = 128; p.bk = 128; break;
     case K_DMA8_128x128_24: p.bm = 128; p.bn = 128; p.bk = 128; break;
+    case K_DMA_64x64: p.bm = 64; p.bn = 64; p.bk = 128; break;
+    case K_DMA_64x128: p.bm = 64; p.bn = 128; p.bk = 128; break;
     default: p.kind = K_TILE_128x128; p.bm = 128; p.bn = 128; p.bk = 128; break;
   }
   if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0 && p.kind != K_TILE_128x128) {
@@ -924,15 +960,7 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   p.splits = 1;
   p.k_split = (int)K;
   int want = forced_splits();
-  if (want <= 0 && forced_kind() < 0 && M <= 64 &&
-      (p.kind == K_DMA_128x128 || p.kind == K_DMA8_128x128_24) &&
-      ceil_div(M, 128) * ceil_div(N, 128) <= 128 && K / p.bk >= 16) {
-    // At most half the CUs would hold a tile: two K halves (int32 partials
-    // summed by gemm_finalize) use all of them. 33..64 x 11008 x 4096:
-    // 20-21 us -> 15-17.5 us. Not with 172 tiles (N = 22016), and not from
-    // M = 128 on, where the partial traffic outweighs the gain.
-    want = 2;
-  }
+  if (want <= 0 && fill_splits > 0) want = fill_splits;
   if (want > 1 && p.kind != K_TILE_128x128) {
     const int64_t kt = K / p.bk;
     const int64_t per = ceil_div(kt, want);
@@ -977,6 +1005,8 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
     case K_DMA8_256x128: SI_DMA(256, 128, 64, 4, 2, 4); break;
     case K_DMA8_128x128_42: SI_DMA(128, 128, 128, 4, 2, 4); break;
     case K_DMA8_128x128_24: SI_DMA(128, 128, 128, 2, 4, 4); break;
+    case K_DMA_64x64: SI_DMA(64, 64, 128, 2, 2, 4); break;
+    case K_DMA_64x128: SI_DMA(64, 128, 128, 2, 2, 4); break;
     default: SI_DMA(128, 256, 64, 2, 4, 4); break;
   }
 #undef SI_DMA

@@ -1,5 +1,5 @@
 """Seeded random shapes through every INT8 GEMM path the tile choice can take
-(weight streaming at several column widths, split K, 128x128 / 256x128 /
+(weight streaming at several column widths, split K, 64x64 / 64x128 / 128x128 / 256x128 /
 256x192 / 256x256 tiles, the register-staged tile for K not a multiple of 64,
 the scalar kernel for K not a multiple of 16): int32 results against the exact
 float64 product, and the INT8Linear epilogue (int8_linear.py:102-115) against
