@@ -85,8 +85,11 @@ def test_workspace_queries():
     # small M streams the weight with K split inside the block: no partials
     assert _native.size_query("si_gemm_workspace_bytes", 16, 11008, 4096) == 0
     assert _native.size_query("si_gemm_workspace_bytes", 2048, 11008, 4096) == 0
-    # a 64-row GEMM over 11008 columns splits K in two: int32 partials [2, M, N]
-    assert _native.size_query("si_gemm_workspace_bytes", 64, 11008, 4096) == 2 * 64 * 11008 * 4
+    # 64 rows x 11008 columns fill 172 CUs with 64x64 tiles: no K split
+    assert _native.size_query("si_gemm_workspace_bytes", 64, 11008, 4096) == 0
+    # the 4096-column down projection (K = 11008) has 64 such tiles and splits K
+    # in four: int32 partials [4, M, N]
+    assert _native.size_query("si_gemm_workspace_bytes", 48, 4096, 11008) == 4 * 48 * 4096 * 4
     n = 8192 * 32
     assert _native.size_query("si_admit_workspace_bytes", n) >= 5 * n
     assert _native.size_query("si_int8_linear_workspace_bytes", 16, 4096, 11008) >= 16 * 4096
