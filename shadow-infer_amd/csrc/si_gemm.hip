@@ -834,7 +834,8 @@ int forced_splits() {
   return splits;
 }
 
-// Tile and split-K choice for 16 < M <= 128 with K % 128 == 0, where each CU
+// Tile and split-K choice for 16 < M <= 128 with K % 128 == 0 (and up to
+// M = 512 where the larger tiles would leave most CUs idle), where each CU
 // holds at most one block and a block's time is set by how fast its CU can
 // pull A and B rows out of L2 (about 63 GB/s per CU with 4 waves), plus a
 // fixed 6.7 us per wave of blocks; split K adds the int32 partial round trip
@@ -892,12 +893,17 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
                            {K_DMA_256x128_K128, 256, 128, 0.81},
                            {K_DMA8_128x128_24, 128, 128, 0.78}};
     double best = 0.0;
+    int64_t best_tiles = 0;
     kind = K_DMA8_256x192_K128;
     for (const Cand& c : cands) {
       const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn);
       const double t = (double)ceil_div(tiles, 256) * c.bm * c.bn / c.speed;
-      if (best == 0.0 || t < best * (1.0 - 1e-9)) { best = t; kind = c.kind; }
+      if (best == 0.0 || t < best * (1.0 - 1e-9)) { best = t; kind = c.kind; best_tiles = tiles; }
     }
+    // A grid that leaves over half the CUs idle (the 4096-column down
+    // projection: 64-128 tiles up to M = 512) goes to the fill model, which
+    // splits K: 256 x 4096 x 11008 52.3 -> 28.1 us, 512 rows 51.5 -> 41.7 us.
+    if (best_tiles <= 128 && M <= 512) kind = choose_fill(M, N, K, &fill_splits);
   } else if (K % 64 == 0) {
     kind = K_DMA_256x192;
   } else {

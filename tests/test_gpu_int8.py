@@ -65,11 +65,13 @@ def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(256, 4096, 11008), (1024, 4096, 11008),
                                    (2048, 4096, 22016), (2048, 11008, 4096),
                                    (24, 4096, 11008), (48, 11008, 4096), (128, 4096, 11008),
-                                   (128, 11008, 4096), (40, 4096, 22016), (100, 4096, 1000)])
+                                   (128, 11008, 4096), (40, 4096, 22016), (100, 4096, 1000),
+                                   (256, 11008, 4096), (384, 11008, 4096), (200, 4096, 3000)])
 def test_gemm_i32_large_m_exact(dev, M, K, N):
     """FFN shapes (up, fused gate|up and down) against the exact float64 product:
-    large M on the 256-row tiles, and 17..128 rows on the 64x64 / 64x128 /
-    128x128 tiles with and without split K."""
+    large M on the 256-row tiles, 17..128 rows on the 64x64 / 64x128 / 128x128
+    tiles with and without split K, and the down projection split in K up to
+    512 rows."""
     g = torch.Generator().manual_seed(M + K)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
     b = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(dev)
