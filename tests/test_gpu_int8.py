@@ -53,7 +53,8 @@ def _exact_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
                                    (64, 4096, 11008), (33, 256, 48), (300, 512, 272),
                                    (7, 40, 24), (3, 17, 5), (100, 96, 48), (65, 4096, 200),
                                    (900, 1024, 300), (17, 11008, 4096), (16, 11008, 4096),
-                                   (16, 4096, 22016), (3, 512, 5000)])
+                                   (16, 4096, 22016), (3, 512, 5000), (20, 2048, 5),
+                                   (70, 4096, 33), (130, 11008, 7), (500, 2048, 100)])
 def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
     g = torch.Generator().manual_seed(M * 7 + K + N)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
