@@ -804,7 +804,8 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             K_DMA8_128x128_42 = 30, K_DMA8_128x128_24 = 31,
             // weight streaming with 32 / 16 output columns per block
             K_STREAM_N32 = 32, K_STREAM_N16 = 33, K_STREAM_N32_W8 = 34, K_STREAM_N16_W8 = 35,
-            // 64-row tiles for 33 <= M <= 64 (no rows of padding in the A tile)
+            // 64-row tiles of the small-M choice (choose_fill): less row padding and
+            // more blocks than 128x128 when few rows share the weight
             K_DMA_64x64 = 38, K_DMA_64x128 = 39 };
 
 struct Plan {
