@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SI_ABI_VERSION 2
+#define SI_ABI_VERSION 3
 
 #define SI_OK 0
 #define SI_ERR_INVALID 1
@@ -335,13 +335,14 @@ int si_page_write_pages(const void* k, const void* v, int dtype, int64_t B, int6
                         void* const* pages, int64_t capacity, si_stream_t stream);
 
 /* Replaces PagedKVStore.gather / _decode (paged_kv_store.py:326-405): every
- * page of the device table (int64 [n_pages, 8] rows {precision, k, v,
- * scale_k, scale_v, start token, tokens, capacity}) decoded into fp32
- * out_k/out_v [B, H, S, D] at its start token; rows no page covers are left
- * as they are (the caller zeroes them). `dtype`: the input dtype of the pages. */
-int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, int64_t B, int64_t H,
-                   int64_t S, int64_t D, int64_t group, float* out_k, float* out_v,
-                   si_stream_t stream);
+ * page of the device table (int64 [n_pages, 9] rows {precision, dtype, k, v,
+ * scale_k, scale_v, start token, tokens, capacity}; dtype = the page's input
+ * dtype SI_DT_*, in which its scales and "fp32" payloads are stored, so pages
+ * of one store may differ) decoded into fp32 out_k/out_v [B, H, S, D] at its
+ * start token; rows no page covers are left as they are (the caller zeroes
+ * them). */
+int si_page_gather(const int64_t* table, int64_t n_pages, int64_t B, int64_t H, int64_t S,
+                   int64_t D, int64_t group, float* out_k, float* out_v, si_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Rate-distortion admission                                               */
@@ -382,20 +383,31 @@ int si_admit_codes(const int8_t* codes, int8_t* out_codes, int64_t S, int64_t H,
 /* ---------------------------------------------------------------------- */
 
 /* DiffusionLlamaRMSNorm (shadowinfer/models/diffusion_llama.py:311-321) over
- * rows of K (K % 8 == 0, K <= 16384): y = T((x / sqrt(mean(x^2) + eps)) * w)
- * with fp32 arithmetic and one rounding to T = dtype. x [M, K], weight [K] in
- * dtype. Outputs (each optional, at least one): y [M, K] in dtype; q int8
- * [M, K] + scale fp32 [M], the INT8Linear activation quantization of y
+ * rows of K (K % 8 == 0, K <= 16384), following the reference's op chain
+ * x / sqrt(mean(x^2) + eps) * w in T = dtype with every op rounded to T:
+ * var = T(mean(T(x^2))) (fp32 sum), r = T(sqrt(T(var + eps))),
+ * y = T(T(x / r) * w). x [M, K], weight [K] in dtype. Outputs (each optional,
+ * at least one): y [M, K] in dtype; q int8 [M, K] + scale fp32 [M], the
+ * INT8Linear activation quantization of y
  * (shadowinfer/ffn_optimizer/int8_linear.py:96-98), identical to
  * si_act_quant_i8 on y. */
 int si_rmsnorm_rows(const void* x, int dtype, int64_t M, int64_t K, const void* weight,
                     float eps, void* y, int8_t* q, float* scale, si_stream_t stream);
 
+/* The residual add of DiffusionLlamaDecoderLayer.forward
+ * (shadowinfer/models/diffusion_llama.py:421-422) fused with the next
+ * RMSNorm: x_out = T(x + residual) [M, K], then si_rmsnorm_rows on x_out
+ * (same optional outputs y, q, scale). */
+int si_add_rmsnorm_rows(const void* x, const void* residual, int dtype, int64_t M, int64_t K,
+                        const void* weight, float eps, void* x_out, void* y, int8_t* q,
+                        float* scale, si_stream_t stream);
+
 /* RoPE and head split of DiffusionLlamaAttention.forward
  * (shadowinfer/models/diffusion_llama.py:362-373): qkv [B*S, 3*H*D] (q | k | v)
- * -> q, k, v [B, H, S, D]; q and k rotated with the rotate-half tables
- * cos_table, sin_table [S, D] (diffusion_llama.py:505-514), fp32 arithmetic,
- * one rounding. D = 64 or 128; all pointers 16-byte aligned. */
+ * -> q, k, v [B, H, S, D]; q and k rotated as q * cos + rotate_half(q) * sin
+ * in dtype (each product rounded, then the sum) with the rotate-half tables
+ * cos_table, sin_table [S, D] (diffusion_llama.py:505-514). D = 64 or 128;
+ * all pointers 16-byte aligned. */
 int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
                   const void* cos_table, const void* sin_table, void* q, void* k, void* v,
                   si_stream_t stream);
@@ -403,16 +415,37 @@ int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, int64_t H, i
 /* DiffusionLlamaMLP's silu(gate) * up (shadowinfer/models/diffusion_llama.py:332-333)
  * and the down INT8Linear's activation quantization (int8_linear.py:96-98):
  * gate_up [M, 2F] (gate | up) in dtype; h = T(T(silu(g)) * u) [M, F]
- * (optional), q int8 [M, F], scale fp32 [M]. F % 8 == 0, F <= 16384. */
+ * (optional) with silu(g) = g / (1 + expf(-g)) in fp32 as torch computes it,
+ * q int8 [M, F], scale fp32 [M]. F % 8 == 0, F <= 16384. */
 int si_swiglu_quant(const void* gate_up, int dtype, int64_t M, int64_t F, void* h, int8_t* q,
                     float* scale, si_stream_t stream);
 
-/* Per-position argmax and confidence of schedule_round
- * (shadowinfer/execution/block_decoding.py:148-151): tokens[m] = first index of
- * the largest logit of row m (NaN counts as largest); confidence[m] = the max
- * softmax probability 1 / sum_v exp(l_v - l_max), fp32. logits [M, V]. */
+/* Per-position token and confidence of schedule_round
+ * (shadowinfer/execution/block_decoding.py:146-147): probs = softmax(logits)
+ * in the logits' dtype T, (confidence, tokens) = probs.max(-1).
+ * confidence[m] = T(1 / s), s = sum_v expf(l_v - l_max) in fp32, written in T
+ * (the logits' dtype); tokens[m] = the first v whose rounded probability
+ * T(expf(l_v - l_max) / s) equals it. A row with a NaN or +inf logit, or only
+ * -inf logits, gives confidence NaN and token 0. logits [M, V]. */
 int si_row_argmax_conf(const void* logits, int dtype, int64_t M, int64_t V, int64_t* tokens,
-                       float* confidence, si_stream_t stream);
+                       void* confidence, si_stream_t stream);
+
+/* Bytes of device workspace si_reuse_drift needs (independent of n). */
+size_t si_reuse_drift_workspace_bytes(int64_t n);
+
+/* The two reductions of the step-reuse drift gate
+ * (shadowinfer/execution/step_reuse.py:71-80), ||hidden - hidden_in|| and
+ * ||hidden_in|| before their square roots: out[0] = sum T(h - h_in)^2,
+ * out[1] = sum h_in^2, fp32 accumulation (device float[2]); h, h_in: n
+ * elements in dtype T, 16-byte aligned. Deterministic for a given n. */
+int si_reuse_drift(const void* hidden, const void* hidden_in, int dtype, int64_t n, float* out,
+                   void* workspace, size_t workspace_bytes, si_stream_t stream);
+
+/* The reused block output of DiffusionTransformerBlock.forward
+ * (shadowinfer/models/simple_diffusion_llm.py:104):
+ * out = T(hidden_out + T(hidden - hidden_in)), n elements in dtype T. */
+int si_reuse_apply(const void* hidden, const void* hidden_in, const void* hidden_out, int dtype,
+                   int64_t n, void* out, si_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,9 @@ Usage: ``python shadow-infer_amd/build.py`` (also called by
 ``__graft_entry__.build()``). Each ``csrc/*.hip`` file is compiled to an
 object in parallel, then linked into
 ``shadowinfer_amd/_lib/libshadowinfer_hip.so`` next to the Python package, so
-the library travels with the source tree.
+the library travels with the source tree. The small host extension
+``_hostmask`` (csrc/host_masks.c) is built next to it with the system C
+compiler.
 """
 
 from __future__ import annotations
@@ -14,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -43,6 +46,25 @@ CFLAGS = [
 
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build_host_ext(verbose: bool = False) -> str:
+    """The CPython extension ``_hostmask`` (csrc/host_masks.c): the reference's
+    set / dict token-head arguments as dense masks. Plain host C, built with
+    the system compiler against this interpreter's headers."""
+    inc = sysconfig.get_paths()["include"]
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(OUT_DIR, "_hostmask" + suffix)
+    tmp = out + ".tmp%d" % os.getpid()
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-shared", "-fPIC", "-Wall", f"-I{inc}",
+           os.path.join(CSRC, "host_masks.c"), "-o", tmp, "-lm"]
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("host extension build failed:\n" + proc.stdout)
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
 
 
 def _compile(src: str) -> str:
@@ -76,6 +98,7 @@ def build(verbose: bool = False) -> str:
     shutil.rmtree(OBJ_DIR, ignore_errors=True)
     if verbose:
         print(f"built {lib}")
+    build_host_ext(verbose)
     return lib
 
 

@@ -1372,9 +1372,13 @@ __global__ __launch_bounds__(256) void page_write_generic(const void* __restrict
 
 // One page-table row: precision, k, v, scale_k, scale_v, start token, tokens,
 // capacity (int64 each).
+// One row of the device page table: precision, the page's input dtype (the
+// dtype of its scales and of "fp32" payloads), payload and scale pointers,
+// first token, tokens held, capacity in rows.
 struct PageRow {
-  int64_t prec, k, v, sk, sv, start, ntok, cap;
+  int64_t prec, dt, k, v, sk, sv, start, ntok, cap;
 };
+constexpr int kPageRowWords = 9;
 
 template <int SDT>
 __device__ __forceinline__ float page_value(const PageRow& pr, int j, int64_t row, int64_t d,
@@ -1456,17 +1460,14 @@ __device__ __forceinline__ void gather_page_vec(const PageRow& pr, int64_t bh, i
 }
 
 // gather (:326-405): every page's rows decoded to fp32 [B, H, S, D] in one
-// launch. Grid: blockIdx.x = page, blockIdx.y = b*H + h. VEC: four values of
-// one group per thread, loads and 16-byte stores specialised for the page's
-// precision (D % 4 == 0, group % 4 == 0, 16-byte aligned rows).
+// launch. Grid: blockIdx.x = page, blockIdx.y = b*H + h; each block reads its
+// page's input dtype from the table (pages of one store may differ). VEC: four
+// values of one group per thread, loads and 16-byte stores specialised for the
+// page's precision (D % 4 == 0, group % 4 == 0, 16-byte aligned rows).
 template <int SDT, bool VEC>
-__global__ __launch_bounds__(256) void page_gather_kernel(const int64_t* __restrict__ table,
-                                                          int64_t S, int64_t D, int64_t g,
-                                                          float* __restrict__ ok,
-                                                          float* __restrict__ ov) {
-  const int64_t* t = table + (int64_t)blockIdx.x * 8;
-  const PageRow pr{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
-  const int64_t bh = blockIdx.y;
+__device__ __forceinline__ void gather_page(const PageRow& pr, int64_t bh, int64_t S, int64_t D,
+                                            int64_t g, float* __restrict__ ok,
+                                            float* __restrict__ ov) {
   if constexpr (VEC) {
     switch ((int)pr.prec) {
       case SI_PREC_FP32: gather_page_vec<SDT, SI_PREC_FP32>(pr, bh, S, (int)D, (int)g, ok, ov); break;
@@ -1484,6 +1485,21 @@ __global__ __launch_bounds__(256) void page_gather_kernel(const int64_t* __restr
       ok[o] = page_value<SDT>(pr, 0, row, d, D, g);
       ov[o] = page_value<SDT>(pr, 1, row, d, D, g);
     }
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void page_gather_kernel(const int64_t* __restrict__ table,
+                                                          int64_t S, int64_t D, int64_t g,
+                                                          float* __restrict__ ok,
+                                                          float* __restrict__ ov) {
+  const int64_t* t = table + (int64_t)blockIdx.x * kPageRowWords;
+  const PageRow pr{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8]};
+  const int64_t bh = blockIdx.y;
+  switch ((int)pr.dt) {
+    case SI_DT_F32: gather_page<SI_DT_F32, VEC>(pr, bh, S, D, g, ok, ov); break;
+    case SI_DT_F16: gather_page<SI_DT_F16, VEC>(pr, bh, S, D, g, ok, ov); break;
+    default: gather_page<SI_DT_BF16, VEC>(pr, bh, S, D, g, ok, ov); break;
   }
 }
 
@@ -1842,11 +1858,10 @@ extern "C" int si_page_write_pages(const void* k, const void* v, int dtype, int6
                         capacity, 0, n_pages, stream);
 }
 
-extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, int64_t B,
-                              int64_t H, int64_t S, int64_t D, int64_t group, float* out_k,
-                              float* out_v, si_stream_t stream) {
+extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int64_t B, int64_t H,
+                              int64_t S, int64_t D, int64_t group, float* out_k, float* out_v,
+                              si_stream_t stream) {
   clear_error();
-  SI_CHECK_ARG(dtype_ok(dtype), "si_page_gather: unsupported dtype %d", dtype);
   SI_CHECK_ARG(n_pages >= 0 && B >= 0 && H >= 0 && S >= 0 && D > 0, "si_page_gather: bad shape");
   SI_CHECK_ARG(group > 0 && D % group == 0, "si_page_gather: group must divide D");
   if (n_pages == 0 || B * H == 0) return SI_OK;
@@ -1859,15 +1874,8 @@ extern "C" int si_page_gather(const int64_t* table, int64_t n_pages, int dtype, 
   const bool vec = D % 4 == 0 && group % 4 == 0 && D < (1 << 20) &&
                    ((reinterpret_cast<uintptr_t>(out_k) | reinterpret_cast<uintptr_t>(out_v)) & 15) == 0;
   hipStream_t st = as_stream(stream);
-#define SI_PG(SDT_)                                                                          \
-  do {                                                                                       \
-    if (vec) page_gather_kernel<SDT_, true><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);  \
-    else page_gather_kernel<SDT_, false><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);     \
-  } while (0)
-  if (dtype == SI_DT_F32) SI_PG(SI_DT_F32);
-  else if (dtype == SI_DT_F16) SI_PG(SI_DT_F16);
-  else SI_PG(SI_DT_BF16);
-#undef SI_PG
+  if (vec) page_gather_kernel<true><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);
+  else page_gather_kernel<false><<<grid, 256, 0, st>>>(table, S, D, group, out_k, out_v);
   return check_launch("si_page_gather");
 }
 

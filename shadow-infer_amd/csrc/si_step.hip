@@ -41,6 +41,17 @@ __device__ __forceinline__ float block_absmax(float m, float* lds) {
   return r;
 }
 
+// Block-wide maximum over 256 threads (NaN-free inputs); every thread gets it.
+__device__ __forceinline__ float block_max(float m, float* lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = m;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+  __syncthreads();
+  return r;
+}
+
 template <int DT>
 __device__ __forceinline__ void load8(const void* p, int64_t i, float* v) {
   if constexpr (DT == SI_DT_F32) {
@@ -111,17 +122,25 @@ __device__ __forceinline__ void quant_row(float (&v)[R][8], int nch, int64_t row
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm (DiffusionLlamaRMSNorm, diffusion_llama.py:311-321) over rows of K:
-//   y = T((x * (1 / sqrt(mean(x^2) + eps))) * w)
-// with the mean of squares in fp32 (one rounding to T at the end). Optional
-// outputs: y [M, K] in T, and the INT8Linear quantization of y (q int8 [M, K],
-// scale fp32 [M]) -- the input of a quantized projection, bit-identical to
-// si_act_quant_i8 on y. One block per row, the row in registers (K <= 2048 R).
+// RMSNorm (DiffusionLlamaRMSNorm, diffusion_llama.py:311-321) over rows of K,
+// following the reference's op chain in the row dtype T, every op rounded to T:
+//   var = T(mean(T(x^2)))          (fp32 sum, then * factor as torch's mean)
+//   r   = T(sqrt(T(var + eps)))
+//   y   = T(T(x / r) * w)
+// factor is torch's mean factor float(M) / float(M * K) (1/K when exact).
+// With RESID, x is first replaced by T(x + resid) (the residual add of
+// DiffusionLlamaDecoderLayer.forward, diffusion_llama.py:421-423), which is
+// also written to xo. Optional outputs: y [M, K] in T, and the INT8Linear
+// quantization of y (q int8 [M, K], scale fp32 [M]) -- the input of a quantized
+// projection, bit-identical to si_act_quant_i8 on y. One block per row, the
+// row in registers (K <= 2048 R).
 // ---------------------------------------------------------------------------
-template <int DT, int R>
+template <int DT, int R, bool RESID>
 __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
+                                                    const void* __restrict__ res,
                                                     const void* __restrict__ w, int64_t M, int K,
-                                                    float eps, void* __restrict__ y,
+                                                    float factor, float eps,
+                                                    void* __restrict__ xo, void* __restrict__ y,
                                                     int8_t* __restrict__ q,
                                                     float* __restrict__ scale) {
   __shared__ float lds[4];
@@ -134,15 +153,23 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
       const int c = (int)threadIdx.x + r * 256;
       if (c < nch) {
         load8<DT>(x, m * K + (int64_t)c * 8, v[r]);
+        if constexpr (RESID) {
+          float o[8];
+          load8<DT>(res, m * K + (int64_t)c * 8, o);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[r][e] * v[r][e];
+          for (int e = 0; e < 8; ++e) v[r][e] = round_to(v[r][e] + o[e], DT);
+          store8<DT>(xo, m * K + (int64_t)c * 8, v[r]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += round_to(v[r][e] * v[r][e], DT);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[r][e] = 0.0f;
       }
     }
     ss = block_sum(ss, lds);
-    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    const float var = round_to(ss * factor, DT);
+    const float rs = round_to(sqrtf(round_to(var + eps, DT)), DT);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int c = (int)threadIdx.x + r * 256;
@@ -150,7 +177,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
       float wv[8];
       load8<DT>(w, (int64_t)c * 8, wv);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[r][e] = round_to((v[r][e] * inv) * wv[e], DT);
+      for (int e = 0; e < 8; ++e) v[r][e] = round_to(round_to(v[r][e] / rs, DT) * wv[e], DT);
       if (y != nullptr) store8<DT>(y, m * K + (int64_t)c * 8, v[r]);
     }
     if (q != nullptr) quant_row<R>(v, nch, m, K, q, scale, lds);
@@ -160,11 +187,13 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
 // ---------------------------------------------------------------------------
 // RoPE + head split (DiffusionLlamaAttention.forward, diffusion_llama.py:362-373):
 // qkv [B*S, 3*H*D] (q | k | v column blocks, each [H, D]) ->
-// q, k, v [B, H, S, D], q and k rotated:
-//   out[d]       = T(x[d] cos[s,d] - x[d+D/2] sin[s,d])
-//   out[d+D/2]   = T(x[d+D/2] cos[s,d+D/2] + x[d] sin[s,d+D/2])    (d < D/2)
+// q, k, v [B, H, S, D], q and k rotated as the reference's
+// q * cos + rotate_half(q) * sin in the row dtype T (each product rounded to
+// T, then the sum rounded to T):
+//   out[d]       = T(T(x[d] cos[s,d]) - T(x[d+D/2] sin[s,d]))
+//   out[d+D/2]   = T(T(x[d+D/2] cos[s,d+D/2]) + T(x[d] sin[s,d+D/2]))   (d < D/2)
 // with the cos/sin tables [S, D] in T (the reference's emb = cat(freqs, freqs)
-// cast to the parameter dtype) and fp32 arithmetic, one rounding.
+// cast to the parameter dtype).
 // A thread owns 8 dims of the first half and their 8 partners.
 // ---------------------------------------------------------------------------
 template <int DT, int D>
@@ -199,8 +228,8 @@ __global__ __launch_bounds__(256) void rope_split(const void* __restrict__ qkv,
       load8<DT>(qkv, in + part * H * D + HALF, x1);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        y0[e] = round_to(x0[e] * c0[e] - x1[e] * s0[e], DT);
-        y1[e] = round_to(x1[e] * c1[e] + x0[e] * s1[e], DT);
+        y0[e] = round_to(round_to(x0[e] * c0[e], DT) - round_to(x1[e] * s0[e], DT), DT);
+        y1[e] = round_to(round_to(x1[e] * c1[e], DT) + round_to(x0[e] * s1[e], DT), DT);
       }
       void* dst = part == 0 ? qo : ko;
       store8<DT>(dst, out, y0);
@@ -215,10 +244,39 @@ __global__ __launch_bounds__(256) void rope_split(const void* __restrict__ qkv,
 }
 
 // ---------------------------------------------------------------------------
+// silu(g) rounded to T as torch computes it: T(g / (1 + expf(-g))) in fp32
+// with IEEE division and the library expf.
+// For T = bf16/fp16 a fast form f = g * rcp(1 + exp2(-g log2e)) (v_exp_f32,
+// v_rcp_f32) is used when it provably rounds the same way. Its distance to the
+// fp32 quotient E is below B = (|g| 2^-22 + 2^-19) |f|: the rounded constant
+// and product -g log2e move the exponent by at most |g| log2e 2^-23 (a
+// relative error of at most |g| 2^-23 in exp); v_exp_f32, v_rcp_f32 and the
+// library expf add one ulp (2^-23) each, and the roundings of the two sums,
+// the product and the quotient half an ulp each (6e-7 in all, below
+// 2^-19 = 1.9e-6). If f - 2B and f + 2B round to
+// the same T value, E does too; otherwise (a T rounding midpoint lies in the
+// interval, about 0.2% of elements for bf16) E itself is computed. |g| >= 64,
+// NaN and infinities always take the exact path.
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float silu_rounded(float g) {
+  if constexpr (DT == SI_DT_F32) {
+    return g / (1.0f + expf(-g));
+  } else {
+    const float ex = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+    const float f = g * __builtin_amdgcn_rcpf(1.0f + ex);
+    const float b = 2.0f * fabsf(f) * (fabsf(g) * 0x1p-22f + 0x1p-19f);
+    const float lo = round_to(f - b, DT);
+    if (lo == round_to(f + b, DT) && fabsf(g) < 64.0f) return lo;
+    return round_to(g / (1.0f + expf(-g)), DT);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // SwiGLU + down-projection input quantization (DiffusionLlamaMLP.forward,
 // diffusion_llama.py:332-333; the down INT8Linear prologue int8_linear.py:96-98):
-// gu [M, 2F] holds gate | up; h = T(T(silu(g)) * u), silu(g) = g / (1 + exp(-g))
-// in fp32 (torch's two elementwise ops, each rounded to T). Writes h [M, F]
+// gu [M, 2F] holds gate | up; h = T(T(silu(g)) * u) (torch's two elementwise
+// ops, each rounded to T; silu as silu_rounded). Writes h [M, F]
 // (optional) and its INT8Linear quantization q int8 [M, F], scale fp32 [M].
 // ---------------------------------------------------------------------------
 template <int DT, int R>
@@ -238,17 +296,7 @@ __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu,
         load8<DT>(gu, m * 2 * F + F + (int64_t)c * 8, u);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float sg;
-          if constexpr (DT == SI_DT_F32) {
-            sg = g[e] / (1.0f + expf(-g[e]));
-          } else {
-            // g / (1 + exp(-g)) with v_exp_f32 and v_rcp_f32: a few fp32 ulps from
-            // the correctly rounded quotient, below half a bf16/fp16 ulp, before
-            // the rounding to T
-            const float ex = __builtin_amdgcn_exp2f(-g[e] * 1.44269504088896341f);
-            sg = round_to(g[e] * __builtin_amdgcn_rcpf(1.0f + ex), DT);
-          }
-          v[r][e] = round_to(sg * u[e], DT);
+          v[r][e] = round_to(silu_rounded<DT>(g[e]) * u[e], DT);
         }
         if (h != nullptr) store8<DT>(h, m * F + (int64_t)c * 8, v[r]);
       } else {
@@ -261,93 +309,222 @@ __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu,
 }
 
 // ---------------------------------------------------------------------------
-// Per-position argmax and confidence (schedule_round, block_decoding.py:148-151):
-// tok[m] = the first index of the largest logit (a NaN counts as largest),
-// conf[m] = max softmax probability = 1 / sum_v exp(l_v - l_max), in fp32.
-// One block per row, one pass: each thread keeps its best (value, index) and
-// the sum of exp(l - its running max), rescaled when the max grows; partial
-// results merge by the same rule. 16-byte loads when rows allow.
+// Per-position token and confidence of schedule_round
+// (block_decoding.py:146-147): probs = softmax(logits) in the logits' dtype T,
+// then (conf, tok) = probs.max(-1), which takes the first index among equal
+// maxima. torch's softmax computes p_v = T(expf(l_v - m) / s) with m the row
+// max and s = sum_v expf(l_v - m) in fp32, so
+//   conf = T(1 / s)                                  (expf(0) = 1)
+//   tok  = first v with T(expf(l_v - m) / s) == conf
+// Ties after the rounding to T are common for bf16 logits, and they resolve to
+// the first index, not to the largest logit. Only logits within 1/16 of m can
+// tie (a tie needs expf(l_v - m) >= 1 - 2^-7 for bf16, closer for fp16/fp32).
+// A row holding a NaN or +inf, or only -inf, has NaN probabilities: conf NaN,
+// tok 0 (the first NaN).
+// One block per row, three passes over the row (max; sum; first tie), the
+// later two from L2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool beats(float a, int64_t ia, float b, int64_t ib) {
-  const bool na = a != a, nb = b != b;
-  if (na || nb) return na && (!nb || ia < ib);
-  return a > b || (a == b && ia < ib);
-}
-
-struct ArgSum {
-  float m;     // running max (NaN once a NaN was seen)
-  int64_t i;   // its first index
-  float s;     // sum of exp(l - m)
-};
-
-__device__ __forceinline__ void arg_add(ArgSum& a, float x, int64_t i) {
-  if (beats(x, i, a.m, a.i)) {
-    if (x != a.m) a.s = a.m == -INFINITY ? 0.0f : a.s * expf(a.m - x);
-    a.m = x;
-    a.i = i;
+template <int DT, bool VEC, typename F>
+__device__ __forceinline__ void for_row(const void* __restrict__ logits, int64_t m, int64_t V,
+                                        F&& f) {
+  if constexpr (VEC) {
+    for (int64_t c = threadIdx.x; c < V / 8; c += blockDim.x) {
+      float v[8];
+      load8<DT>(logits, m * V + c * 8, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f(v[e], c * 8 + e);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < V; i += blockDim.x) f(load_any(logits, DT, m * V + i), i);
   }
-  a.s += x == -INFINITY ? 0.0f : expf(x - a.m);
-}
-
-__device__ __forceinline__ void arg_merge(ArgSum& a, const ArgSum& b) {
-  const float m = beats(b.m, b.i, a.m, a.i) ? b.m : a.m;
-  const float sa = a.m == -INFINITY ? 0.0f : a.s * expf(a.m - m);
-  const float sb = b.m == -INFINITY ? 0.0f : b.s * expf(b.m - m);
-  if (beats(b.m, b.i, a.m, a.i)) a.i = b.i;
-  a.m = m;
-  a.s = sa + sb;
 }
 
 template <int DT, bool VEC>
 __global__ __launch_bounds__(256) void row_argmax_conf(const void* __restrict__ logits,
                                                        int64_t M, int64_t V,
                                                        int64_t* __restrict__ tok,
-                                                       float* __restrict__ conf) {
-  __shared__ float lm[4], ls[4];
-  __shared__ int64_t li[4];
+                                                       void* __restrict__ conf) {
+  __shared__ float lds[4];
+  __shared__ int64_t ldi[4];
   for (int64_t m = blockIdx.x; m < M; m += gridDim.x) {
-    ArgSum a{-INFINITY, INT64_MAX, 0.0f};
-    if constexpr (VEC) {
-      for (int64_t c = threadIdx.x; c < V / 8; c += blockDim.x) {
-        float v[8];
-        load8<DT>(logits, m * V + c * 8, v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) arg_add(a, v[e], c * 8 + e);
+    // pass 1: the row max, and whether the softmax is NaN everywhere
+    float mx = -INFINITY;
+    float bad = 0.0f;
+    for_row<DT, VEC>(logits, m, V, [&](float x, int64_t) {
+      if (x != x || x == INFINITY) bad = 1.0f;
+      mx = fmaxf(mx, x);
+    });
+    mx = block_max(mx, lds);
+    bad = block_sum(bad, lds);
+    if (bad != 0.0f || mx == -INFINITY) {
+      if (threadIdx.x == 0) {
+        tok[m] = 0;
+        store_any(conf, DT, m, __uint_as_float(0x7fc00000u));
       }
-    } else {
-      for (int64_t v = threadIdx.x; v < V; v += blockDim.x) arg_add(a, load_any(logits, DT, m * V + v), v);
+      continue;
     }
+    // pass 2: the sum of exponentials
+    float s = 0.0f;
+    for_row<DT, VEC>(logits, m, V, [&](float x, int64_t) { s += expf(x - mx); });
+    s = block_sum(s, lds);
+    const float c = round_to(1.0f / s, DT);
+    // pass 3: the first index whose rounded probability equals c
+    int64_t first = INT64_MAX;
+    for_row<DT, VEC>(logits, m, V, [&](float x, int64_t i) {
+      if (i < first && x - mx >= -0.0625f && round_to(expf(x - mx) / s, DT) == c) first = i;
+    });
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-      ArgSum b{__shfl_xor(a.m, off, 64), __shfl_xor(a.i, off, 64), __shfl_xor(a.s, off, 64)};
-      arg_merge(a, b);
+      const int64_t o = __shfl_xor(first, off, 64);
+      first = o < first ? o : first;
     }
-    if ((threadIdx.x & 63) == 0) {
-      lm[threadIdx.x >> 6] = a.m;
-      li[threadIdx.x >> 6] = a.i;
-      ls[threadIdx.x >> 6] = a.s;
-    }
+    if ((threadIdx.x & 63) == 0) ldi[threadIdx.x >> 6] = first;
     __syncthreads();
     if (threadIdx.x == 0) {
-      ArgSum r{lm[0], li[0], ls[0]};
-      for (int w = 1; w < 4; ++w) arg_merge(r, ArgSum{lm[w], li[w], ls[w]});
-      tok[m] = r.i == INT64_MAX ? 0 : r.i;
-      conf[m] = 1.0f / r.s;
+      int64_t r = ldi[0];
+      for (int w = 1; w < 4; ++w) r = ldi[w] < r ? ldi[w] : r;
+      tok[m] = r;
+      store_any(conf, DT, m, c);
     }
     __syncthreads();
   }
 }
 
-unsigned row_grid(int64_t M) { return (unsigned)(M < 262144 ? (M < 1 ? 1 : M) : 262144); }
+// ---------------------------------------------------------------------------
+// Cross-step block reuse (execution/step_reuse.py:71-95,
+// models/simple_diffusion_llm.py:104): the drift gate's two sums and the
+// reused hidden state.
+//   reuse_partial : per block, sum T(h - h_in)^2 and sum h_in^2 in fp32 over
+//                   a grid-strided share of n elements (8 per load), then
+//   reuse_final   : one block adds the block partials in a fixed order.
+// The result is deterministic for a given n. The caller takes the square
+// roots and the ratio (torch's norm: fp32 accumulation, one rounding to T).
+//   reuse_apply   : out = T(h_out + T(h - h_in)), the reference's two ops.
+// ---------------------------------------------------------------------------
+constexpr int kReuseBlocks = 1024;
 
 template <int DT>
-void launch_rmsnorm(const void* x, const void* w, int64_t M, int K, float eps, void* y, int8_t* q,
-                    float* s, hipStream_t st) {
+__global__ __launch_bounds__(256) void reuse_partial(const void* __restrict__ h,
+                                                     const void* __restrict__ hin, int64_t n,
+                                                     float* __restrict__ part) {
+  __shared__ float lds[4];
+  float a = 0.0f, b = 0.0f;
+  const int64_t nch = n / 8;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < nch;
+       c += (int64_t)gridDim.x * 256) {
+    float x[8], y[8];
+    load8<DT>(h, c * 8, x);
+    load8<DT>(hin, c * 8, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = round_to(x[e] - y[e], DT);
+      a += d * d;
+      b += y[e] * y[e];
+    }
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t i = nch * 8 + threadIdx.x; i < n; i += 256) {
+      const float y = load_any(hin, DT, i);
+      const float d = round_to(load_any(h, DT, i) - y, DT);
+      a += d * d;
+      b += y * y;
+    }
+  }
+  a = block_sum(a, lds);
+  b = block_sum(b, lds);
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = a;
+    part[gridDim.x + blockIdx.x] = b;
+  }
+}
+
+__global__ __launch_bounds__(256) void reuse_final(const float* __restrict__ part, int nb,
+                                                   float* __restrict__ out) {
+  __shared__ float lds[4];
+  float a = 0.0f, b = 0.0f;
+  for (int i = threadIdx.x; i < nb; i += 256) {
+    a += part[i];
+    b += part[nb + i];
+  }
+  a = block_sum(a, lds);
+  b = block_sum(b, lds);
+  if (threadIdx.x == 0) {
+    out[0] = a;
+    out[1] = b;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void reuse_apply(const void* __restrict__ h,
+                                                   const void* __restrict__ hin,
+                                                   const void* __restrict__ hout, int64_t n,
+                                                   void* __restrict__ out) {
+  const int64_t nch = n / 8;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < nch;
+       c += (int64_t)gridDim.x * 256) {
+    float x[8], y[8], z[8];
+    load8<DT>(h, c * 8, x);
+    load8<DT>(hin, c * 8, y);
+    load8<DT>(hout, c * 8, z);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = round_to(z[e] + round_to(x[e] - y[e], DT), DT);
+    store8<DT>(out, c * 8, z);
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t i = nch * 8 + threadIdx.x; i < n; i += 256) {
+      const float d = round_to(load_any(h, DT, i) - load_any(hin, DT, i), DT);
+      store_any(out, DT, i, load_any(hout, DT, i) + d);
+    }
+  }
+}
+
+unsigned row_grid(int64_t M) { return (unsigned)(M < 262144 ? (M < 1 ? 1 : M) : 262144); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int DT, bool RESID>
+void launch_rmsnorm(const void* x, const void* res, const void* w, int64_t M, int K, float factor,
+                    float eps, void* xo, void* y, int8_t* q, float* s, hipStream_t st) {
   const unsigned g = row_grid(M);
-  if (K <= 2048) rmsnorm_rows<DT, 1><<<g, 256, 0, st>>>(x, w, M, K, eps, y, q, s);
-  else if (K <= 4096) rmsnorm_rows<DT, 2><<<g, 256, 0, st>>>(x, w, M, K, eps, y, q, s);
-  else if (K <= 8192) rmsnorm_rows<DT, 4><<<g, 256, 0, st>>>(x, w, M, K, eps, y, q, s);
-  else rmsnorm_rows<DT, 8><<<g, 256, 0, st>>>(x, w, M, K, eps, y, q, s);
+  if (K <= 2048)
+    rmsnorm_rows<DT, 1, RESID><<<g, 256, 0, st>>>(x, res, w, M, K, factor, eps, xo, y, q, s);
+  else if (K <= 4096)
+    rmsnorm_rows<DT, 2, RESID><<<g, 256, 0, st>>>(x, res, w, M, K, factor, eps, xo, y, q, s);
+  else if (K <= 8192)
+    rmsnorm_rows<DT, 4, RESID><<<g, 256, 0, st>>>(x, res, w, M, K, factor, eps, xo, y, q, s);
+  else
+    rmsnorm_rows<DT, 8, RESID><<<g, 256, 0, st>>>(x, res, w, M, K, factor, eps, xo, y, q, s);
+}
+
+// torch's mean factor for M rows of K: float(M) / float(M * K) (ATen's
+// mean_kernel_impl), equal to 1/K whenever M * K is exact in fp32.
+float mean_factor(int64_t M, int64_t K) { return (float)M / (float)(M * K); }
+
+template <bool RESID>
+int rmsnorm_entry(const char* name, const void* x, const void* res, int dtype, int64_t M,
+                  int64_t K, const void* weight, float eps, void* xo, void* y, int8_t* q,
+                  float* scale, si_stream_t stream) {
+  SI_CHECK_ARG(dtype == SI_DT_BF16 || dtype == SI_DT_F16 || dtype == SI_DT_F32,
+               "%s: unsupported dtype %d", name, dtype);
+  SI_CHECK_ARG(M >= 0 && K > 0 && K % 8 == 0 && K <= 16384,
+               "%s: K must be a multiple of 8 in [8, 16384] (got %lld)", name, (long long)K);
+  SI_CHECK_ARG((q == nullptr) == (scale == nullptr), "%s: q and scale are given together", name);
+  if (M == 0) return SI_OK;
+  SI_CHECK_ARG(x && weight && (y || q) && (!RESID || (res && xo)), "%s: NULL argument", name);
+  SI_CHECK_ARG(aligned16(x) && aligned16(weight) && (!y || aligned16(y)) &&
+                   (!RESID || (aligned16(res) && aligned16(xo))) &&
+                   (!q || (reinterpret_cast<uintptr_t>(q) & 7) == 0),
+               "%s: x, residual, weight, x_out and y must be 16-byte aligned, q 8-byte aligned",
+               name);
+  hipStream_t st = as_stream(stream);
+  const float f = mean_factor(M, K);
+  if (dtype == SI_DT_BF16)
+    launch_rmsnorm<SI_DT_BF16, RESID>(x, res, weight, M, (int)K, f, eps, xo, y, q, scale, st);
+  else if (dtype == SI_DT_F16)
+    launch_rmsnorm<SI_DT_F16, RESID>(x, res, weight, M, (int)K, f, eps, xo, y, q, scale, st);
+  else
+    launch_rmsnorm<SI_DT_F32, RESID>(x, res, weight, M, (int)K, f, eps, xo, y, q, scale, st);
+  return check_launch(name);
 }
 
 template <int DT>
@@ -369,7 +546,6 @@ void launch_rope(const void* qkv, const void* c, const void* s, int64_t B, int64
   else rope_split<DT, 128><<<g, 256, 0, st>>>(qkv, c, s, B, S, H, q, k, v);
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
 }  // namespace si
@@ -379,21 +555,16 @@ using namespace si;
 extern "C" int si_rmsnorm_rows(const void* x, int dtype, int64_t M, int64_t K, const void* weight,
                                float eps, void* y, int8_t* q, float* scale, si_stream_t stream) {
   clear_error();
-  SI_CHECK_ARG(dtype == SI_DT_BF16 || dtype == SI_DT_F16 || dtype == SI_DT_F32,
-               "si_rmsnorm_rows: unsupported dtype %d", dtype);
-  SI_CHECK_ARG(M >= 0 && K > 0 && K % 8 == 0 && K <= 16384,
-               "si_rmsnorm_rows: K must be a multiple of 8 in [8, 16384] (got %lld)", (long long)K);
-  SI_CHECK_ARG((q == nullptr) == (scale == nullptr),
-               "si_rmsnorm_rows: q and scale are given together");
-  if (M == 0) return SI_OK;
-  SI_CHECK_ARG(x && weight && (y || q), "si_rmsnorm_rows: NULL argument");
-  SI_CHECK_ARG(aligned16(x) && aligned16(weight) && (!y || aligned16(y)) && (!q || (reinterpret_cast<uintptr_t>(q) & 7) == 0),
-               "si_rmsnorm_rows: x, weight and y must be 16-byte aligned, q 8-byte aligned");
-  hipStream_t st = as_stream(stream);
-  if (dtype == SI_DT_BF16) launch_rmsnorm<SI_DT_BF16>(x, weight, M, (int)K, eps, y, q, scale, st);
-  else if (dtype == SI_DT_F16) launch_rmsnorm<SI_DT_F16>(x, weight, M, (int)K, eps, y, q, scale, st);
-  else launch_rmsnorm<SI_DT_F32>(x, weight, M, (int)K, eps, y, q, scale, st);
-  return check_launch("si_rmsnorm_rows");
+  return rmsnorm_entry<false>("si_rmsnorm_rows", x, nullptr, dtype, M, K, weight, eps, nullptr, y,
+                              q, scale, stream);
+}
+
+extern "C" int si_add_rmsnorm_rows(const void* x, const void* residual, int dtype, int64_t M,
+                                   int64_t K, const void* weight, float eps, void* x_out, void* y,
+                                   int8_t* q, float* scale, si_stream_t stream) {
+  clear_error();
+  return rmsnorm_entry<true>("si_add_rmsnorm_rows", x, residual, dtype, M, K, weight, eps, x_out,
+                             y, q, scale, stream);
 }
 
 extern "C" int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, int64_t H,
@@ -436,7 +607,7 @@ extern "C" int si_swiglu_quant(const void* gate_up, int dtype, int64_t M, int64_
 }
 
 extern "C" int si_row_argmax_conf(const void* logits, int dtype, int64_t M, int64_t V,
-                                  int64_t* tokens, float* confidence, si_stream_t stream) {
+                                  int64_t* tokens, void* confidence, si_stream_t stream) {
   clear_error();
   SI_CHECK_ARG(dtype_ok(dtype), "si_row_argmax_conf: unsupported dtype %d", dtype);
   SI_CHECK_ARG(M >= 0 && V > 0, "si_row_argmax_conf: bad shape");
@@ -456,4 +627,48 @@ extern "C" int si_row_argmax_conf(const void* logits, int dtype, int64_t M, int6
     else row_argmax_conf<SI_DT_F32, false><<<g, 256, 0, st>>>(logits, M, V, tokens, confidence);
   }
   return check_launch("si_row_argmax_conf");
+}
+
+extern "C" size_t si_reuse_drift_workspace_bytes(int64_t n) {
+  (void)n;
+  return 2 * kReuseBlocks * sizeof(float);
+}
+
+extern "C" int si_reuse_drift(const void* hidden, const void* hidden_in, int dtype, int64_t n,
+                              float* out, void* workspace, size_t workspace_bytes,
+                              si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_reuse_drift: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(n >= 0, "si_reuse_drift: bad size");
+  SI_CHECK_ARG(out && workspace, "si_reuse_drift: NULL argument");
+  SI_CHECK_ARG(workspace_bytes >= si_reuse_drift_workspace_bytes(n),
+               "si_reuse_drift: workspace of %zu bytes, need %zu", workspace_bytes,
+               si_reuse_drift_workspace_bytes(n));
+  SI_CHECK_ARG(n == 0 || (hidden && hidden_in && aligned16(hidden) && aligned16(hidden_in)),
+               "si_reuse_drift: hidden and hidden_in must be 16-byte aligned device pointers");
+  hipStream_t st = as_stream(stream);
+  const int nb = (int)std::min<int64_t>(kReuseBlocks, std::max<int64_t>(1, ceil_div(n / 8, 256)));
+  float* part = static_cast<float*>(workspace);
+  if (dtype == SI_DT_BF16) reuse_partial<SI_DT_BF16><<<nb, 256, 0, st>>>(hidden, hidden_in, n, part);
+  else if (dtype == SI_DT_F16) reuse_partial<SI_DT_F16><<<nb, 256, 0, st>>>(hidden, hidden_in, n, part);
+  else reuse_partial<SI_DT_F32><<<nb, 256, 0, st>>>(hidden, hidden_in, n, part);
+  reuse_final<<<1, 256, 0, st>>>(part, nb, out);
+  return check_launch("si_reuse_drift");
+}
+
+extern "C" int si_reuse_apply(const void* hidden, const void* hidden_in, const void* hidden_out,
+                              int dtype, int64_t n, void* out, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_reuse_apply: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(n >= 0, "si_reuse_apply: bad size");
+  if (n == 0) return SI_OK;
+  SI_CHECK_ARG(hidden && hidden_in && hidden_out && out, "si_reuse_apply: NULL argument");
+  SI_CHECK_ARG(aligned16(hidden) && aligned16(hidden_in) && aligned16(hidden_out) && aligned16(out),
+               "si_reuse_apply: pointers must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const unsigned g = (unsigned)std::min<int64_t>(std::max<int64_t>(1, ceil_div(n / 8, 256)), 4096);
+  if (dtype == SI_DT_BF16) reuse_apply<SI_DT_BF16><<<g, 256, 0, st>>>(hidden, hidden_in, hidden_out, n, out);
+  else if (dtype == SI_DT_F16) reuse_apply<SI_DT_F16><<<g, 256, 0, st>>>(hidden, hidden_in, hidden_out, n, out);
+  else reuse_apply<SI_DT_F32><<<g, 256, 0, st>>>(hidden, hidden_in, hidden_out, n, out);
+  return check_launch("si_reuse_apply");
 }

@@ -53,7 +53,7 @@ _SIGNATURES = {
                              _i64, _i64, _vp]),
     "si_page_write_pages": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
                                    _vp, _i64, _vp]),
-    "si_page_gather": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "si_page_gather": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "si_kv_unpack_flat": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp,
                                  _vp, _vp]),
     "si_kv_unpack": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
@@ -88,9 +88,14 @@ _SIGNATURES = {
     "si_admit_codes": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
                               _vp, _vp, _sz, _vp]),
     "si_rmsnorm_rows": (_i32, [_vp, _i32, _i64, _i64, _vp, ctypes.c_float, _vp, _vp, _vp, _vp]),
+    "si_add_rmsnorm_rows": (_i32, [_vp, _vp, _i32, _i64, _i64, _vp, ctypes.c_float, _vp, _vp, _vp,
+                                   _vp, _vp]),
     "si_rope_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "si_swiglu_quant": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp]),
     "si_row_argmax_conf": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp]),
+    "si_reuse_drift_workspace_bytes": (_sz, [_i64]),
+    "si_reuse_drift": (_i32, [_vp, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "si_reuse_apply": (_i32, [_vp, _vp, _vp, _i32, _i64, _vp, _vp]),
     "si_int8_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "si_int8_linear_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                       _sz, _vp]),
@@ -138,8 +143,21 @@ def load_error() -> Optional[str]:
     return _load_error
 
 
+def force_cpu() -> bool:
+    """The reference's switch to its CPU kernels (kernels/dispatcher.py:46-49)."""
+    return os.environ.get("SHADOWINFER_FORCE_CPU_KERNELS", "0") == "1"
+
+
+def _refuse_forced_cpu(what: str) -> None:
+    if force_cpu():
+        raise RuntimeError(
+            f"{what}: SHADOWINFER_FORCE_CPU_KERNELS=1 asks for CPU kernels, and this data "
+            "plane has none (every kernel is HIP); unset it to run on the GPU")
+
+
 def call(name: str, *args) -> None:
     """Invoke ``name`` and raise RuntimeError with the library's message on failure."""
+    _refuse_forced_cpu(name)
     lib = load()
     rc = getattr(lib, name)(*args)
     if rc != 0:
@@ -174,6 +192,7 @@ def torch_dtype(code: int) -> torch.dtype:
 
 def require_device(t: torch.Tensor, what: str) -> None:
     """The data plane runs only as HIP kernels: CPU tensors are an error."""
+    _refuse_forced_cpu(what)
     if t.device.type != "cuda":
         raise RuntimeError(
             f"{what}: tensors must live on a HIP device (got {t.device}); "

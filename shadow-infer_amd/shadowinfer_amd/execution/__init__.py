@@ -5,11 +5,11 @@ LM step on packed KV + INT8 FFN."""
 
 from .denoise import DiffusionLlamaShape, PackedDiffusionLlama, mask_tokens
 from .schedule import ScheduleDecision, argmax_confidence, schedule_round
-from .step_reuse import LayerReuseEntry, StepReuseConfig, StepReuseState
+from .step_reuse import LayerRecord, StepReuseConfig, StepReuseState
 
 __all__ = [
     "DiffusionLlamaShape",
-    "LayerReuseEntry",
+    "LayerRecord",
     "PackedDiffusionLlama",
     "ScheduleDecision",
     "StepReuseConfig",

@@ -23,9 +23,9 @@ composes them the way its parts are defined:
 
 Per computed layer the kernels are: RMSNorm (HIP) -> q|k|v projection (one
 bf16 library GEMM) -> RoPE + head split (HIP) -> KV pack (HIP) -> packed
-attention writing token-major output (HIP) -> o projection with the residual
-add folded into the library GEMM -> RMSNorm fused with the activation
-quantization (HIP) -> gate|up INT8 GEMM (HIP, one GEMM over both weights) ->
+attention writing token-major output (HIP) -> o projection (bf16 library
+GEMM) -> residual add fused with the RMSNorm and the activation quantization
+(HIP) -> gate|up INT8 GEMM (HIP, one GEMM over both weights) ->
 SwiGLU fused with the down projection's activation quantization (HIP) ->
 down INT8 GEMM (HIP) -> residual add.
 
@@ -157,21 +157,21 @@ class PackedDiffusionLlama:
         H, D = c.num_attention_heads, c.head_dim
         T = B * S
         x = hidden.reshape(T, Hd)
-        xn, _, _ = row_ops.rmsnorm(x, L.ln1, c.rms_norm_eps)
+        xn, _, _, _ = row_ops.rmsnorm(x, L.ln1, c.rms_norm_eps)
         qkv = F.linear(xn, L.w_qkv)
         q, k, v = row_ops.rope_split(qkv, cos, sin, B, S, H, D)
         cache = PackedKVCache.pack(k, v, None, group_size=c.int4_group_size,
                                    plan=plan)["packed_kv"]
         attn = packed_attention(q, cache, out_dtype=self.dtype, token_major=True)
-        x1 = torch.addmm(x, attn.view(T, Hd), L.w_o.t())
-        y2, qx, sx = row_ops.rmsnorm(x1, L.ln2, c.rms_norm_eps, want_y=trace is not None,
-                                     want_q=True)
+        o = F.linear(attn.view(T, Hd), L.w_o)
+        y2, qx, sx, x1 = row_ops.rmsnorm(x, L.ln2, c.rms_norm_eps, want_y=trace is not None,
+                                         want_q=True, residual=o)
         gu = row_ops.int8_gemm_dequant(qx, sx, L.gu_q, L.gu_s, self.dtype)
         h, qh, sh = row_ops.swiglu_quant(gu, want_h=trace is not None)
         ffn = row_ops.int8_gemm_dequant(qh, sh, L.dn_q, L.dn_s, self.dtype)
         out = x1 + ffn
         if trace is not None:
-            trace.update(x=x, xn=xn, qkv=qkv, q=q, k=k, v=v, cache=cache, attn=attn, x1=x1,
+            trace.update(x=x, xn=xn, qkv=qkv, q=q, k=k, v=v, cache=cache, attn=attn, o=o, x1=x1,
                          y2=y2, qx=qx, sx=sx, gu=gu, h=h, qh=qh, sh=sh, ffn=ffn, out=out)
         return out.view(B, S, Hd), cache
 
@@ -201,29 +201,24 @@ class PackedDiffusionLlama:
         cos, sin = self.rope_tables(S)
         hidden = F.embedding(x.to(self.device), self.embed)
         kv: Dict[int, PackedKVCache] = {}
+        gated = reuse_state is not None and reuse_config is not None
         if reuse_state is not None:
-            reuse_state.begin_step()
+            reuse_state.new_step()
         for i in range(c.num_hidden_layers):
-            if reuse_state is not None and reuse_config is not None:
-                reuse, drift = reuse_state.should_reuse(i, hidden, step_id, reuse_config)
-                if drift is not None:
-                    reuse_state.last_drifts[i] = drift
-                if reuse:
-                    entry = reuse_state.entries[i]
-                    hidden = entry.hidden_out + (hidden - entry.hidden_in)
-                    reuse_state.last_reused_layers.add(i)
-                    kv[i] = entry.packed_kv
-                    continue
+            record = reuse_state.gate(i, hidden, step_id, reuse_config) if gated else None
+            if record is not None:
+                hidden = reuse_state.reuse(i, record, hidden)
+                kv[i] = record.packed_kv
+                continue
             trace = None
             if traces is not None:
                 trace = traces.setdefault(i, {})
             h_in = hidden
             hidden, cache = self.layer_forward(i, hidden, plans[i], cos, sin, trace)
             if reuse_state is not None:
-                reuse_state.record(i, h_in, hidden, packed_kv=cache)
-                reuse_state.last_computed_layers.add(i)
+                reuse_state.keep(i, h_in, hidden, cache)
             kv[i] = cache
-        hn, _, _ = row_ops.rmsnorm(hidden, self.norm, c.rms_norm_eps)
+        hn, _, _, _ = row_ops.rmsnorm(hidden, self.norm, c.rms_norm_eps)
         logits = F.linear(hn, self.lm_head)
         if traces is not None:
             traces["final"] = {"hidden": hidden, "hn": hn, "logits": logits}
@@ -234,14 +229,52 @@ class PackedDiffusionLlama:
                      confidence_threshold: float = 0.9,
                      reuse_state: Optional[StepReuseState] = None,
                      reuse_config: Optional[StepReuseConfig] = None
-                     ) -> Tuple[ScheduleDecision, Dict[int, PackedKVCache]]:
-        """forward_step + one unmasking round; ``tokens`` (int64 ``[B, S]``)
-        and ``masked`` (bool ``[B, S]``) are updated in place on the device."""
+                     ) -> Tuple[ScheduleDecision, Dict[int, PackedKVCache], torch.Tensor]:
+        """forward_step + one unmasking round (block_decoding.py:497-502 over
+        the whole sequence); ``tokens`` (int64 ``[B, S]``) and ``masked`` (bool
+        ``[B, S]``) are updated in place on the device. Returns the decision,
+        the per-layer packed KV and the step's logits."""
         logits, kv = self.forward_step(tokens, plans, step_id, reuse_state, reuse_config)
         decision = schedule_round(logits, masked, confidence_threshold)
         tokens.copy_(torch.where(decision.unmask, decision.tokens, tokens))
         masked &= ~decision.unmask
-        return decision, kv
+        return decision, kv, logits
+
+    def generate(self, tokens: torch.Tensor, masked: torch.Tensor,
+                 plans: Union[PrecisionPlan, Sequence[PrecisionPlan]], steps: int,
+                 confidence_threshold: float = 0.9,
+                 reuse_state: Optional[StepReuseState] = None,
+                 reuse_config: Optional[StepReuseConfig] = None,
+                 on_step=None) -> Dict[str, torch.Tensor]:
+        """``steps`` denoising steps, then the reference's forced completion
+        (block_decoding.py:493-512): positions still masked after the last
+        round take the argmax of that round's logits. ``tokens``/``masked``
+        are updated in place; the loop never reads the device. Returns device
+        tensors: ``unmasked_per_step`` int64 ``[steps, B]``, ``fallback`` bool
+        ``[steps, B]``, ``forced`` int64 ``[B]`` (positions completed by the
+        argmax) and ``finite`` bool (every logit of every step finite).
+        ``on_step(step, decision, kv, logits)``, when given, sees each step."""
+        if steps < 1:
+            raise ValueError(f"steps must be >= 1, got {steps}")
+        B = tokens.shape[0]
+        dev = tokens.device
+        unmasked = torch.zeros(steps, B, dtype=torch.int64, device=dev)
+        fallback = torch.zeros(steps, B, dtype=torch.bool, device=dev)
+        finite = torch.ones((), dtype=torch.bool, device=dev)
+        logits = None
+        for step in range(steps):
+            d, kv, logits = self.denoise_step(tokens, masked, plans, step, confidence_threshold,
+                                              reuse_state, reuse_config)
+            unmasked[step] = d.unmask.sum(dim=1)
+            fallback[step] = d.progress_fallback
+            finite &= torch.isfinite(logits).all()
+            if on_step is not None:
+                on_step(step, d, kv, logits)
+        forced = masked.sum(dim=1)
+        tokens.copy_(torch.where(masked, logits.argmax(dim=-1), tokens))
+        masked.zero_()
+        return {"unmasked_per_step": unmasked, "fallback": fallback, "forced": forced,
+                "finite": finite}
 
 
 def mask_tokens(batch: int, seq_len: int, mask_fraction: float, config: DiffusionLlamaShape,

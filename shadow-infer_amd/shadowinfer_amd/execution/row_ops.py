@@ -18,12 +18,15 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, want_y: bool = True,
-            want_q: bool = False) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor],
-                                           Optional[torch.Tensor]]:
-    """RMSNorm over the last dim of ``x`` (models/diffusion_llama.py:311-321),
-    optionally fused with INT8Linear's activation quantization of the result
-    (int8_linear.py:96-98). Returns ``(y, q, scale)`` with None for what was
-    not asked."""
+            want_q: bool = False, residual: Optional[torch.Tensor] = None
+            ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor],
+                       Optional[torch.Tensor]]:
+    """RMSNorm over the last dim of ``x`` as the reference's op chain in the
+    row dtype (models/diffusion_llama.py:311-321), optionally preceded by the
+    residual add ``x = x + residual`` (diffusion_llama.py:421-422) and fused
+    with INT8Linear's activation quantization of the result
+    (int8_linear.py:96-98). Returns ``(y, q, scale, x_sum)`` with None for what
+    was not asked (``x_sum`` is the rounded ``x + residual``)."""
     _native.require_device(x, "rmsnorm")
     K = x.shape[-1]
     xf = x.reshape(-1, K).contiguous()
@@ -33,10 +36,21 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, want_y: bool = Tr
     y = torch.empty_like(xf) if want_y else None
     q = torch.empty(M, K, dtype=torch.int8, device=x.device) if want_q else None
     s = torch.empty(M, dtype=torch.float32, device=x.device) if want_q else None
-    _native.call("si_rmsnorm_rows", xf.data_ptr(), _native.dtype_code(x.dtype), M, K,
-                 weight.contiguous().data_ptr(), float(eps), _ptr(y), _ptr(q), _ptr(s),
-                 _native.stream(x.device))
-    return (None if y is None else y.view(x.shape)), q, s
+    if residual is None:
+        xo = None
+        _native.call("si_rmsnorm_rows", xf.data_ptr(), _native.dtype_code(x.dtype), M, K,
+                     weight.contiguous().data_ptr(), float(eps), _ptr(y), _ptr(q), _ptr(s),
+                     _native.stream(x.device))
+    else:
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match x in shape and dtype")
+        rf = residual.reshape(-1, K).contiguous()
+        xo = torch.empty_like(xf)
+        _native.call("si_add_rmsnorm_rows", xf.data_ptr(), rf.data_ptr(),
+                     _native.dtype_code(x.dtype), M, K, weight.contiguous().data_ptr(), float(eps),
+                     xo.data_ptr(), _ptr(y), _ptr(q), _ptr(s), _native.stream(x.device))
+    return ((None if y is None else y.view(x.shape)), q, s,
+            (None if xo is None else xo.view(x.shape)))
 
 
 def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, batch: int, seq: int,

@@ -1,139 +1,174 @@
-"""Cross-step block reuse for diffusion denoising
-(shadowinfer/execution/step_reuse.py:18-134).
+"""Cross-step block reuse on the packed data plane (the drift-gated reuse of
+shadowinfer/execution/step_reuse.py:18-134 as DiffusionTransformerBlock uses
+it, models/simple_diffusion_llm.py:99-120).
 
-Same API and gate as the reference: per layer, the input and output hidden
-states of the last full computation are kept; on a later step a layer is
-skipped when the relative-L2 drift of its input stays within ``threshold``,
-and its output becomes ``hidden_out + (hidden - hidden_in)``. In the packed
-pipeline the layer's KV is the ``PackedKVCache`` of that computation
-(``packed_kv``), so a reused layer neither packs nor attends.
+A computed layer leaves a :class:`LayerRecord`: the hidden state it read, the
+one it wrote and its packed KV cache (kept by reference; the step never
+writes into them afterwards). On a later step the layer is skipped when the
+new input is close to the recorded one, and its output becomes
+``hidden_out + (hidden - hidden_in)``; its KV is the recorded cache, so a
+reused layer neither packs nor attends.
 
-Two additions, both off by default:
+The gate keeps the reference's decision: no reuse when disabled or before
+``warmup_steps``; a record of another shape, or with an all-zero input, is
+dropped and the layer recomputed; otherwise reuse iff
+``||hidden - hidden_in|| / ||hidden_in|| <= threshold`` evaluated as torch
+evaluates it in the hidden dtype (each norm an fp32 sum of squares, square
+root, rounded to the dtype; the quotient rounded to the dtype).
 
-* ``reusable_layers`` restricts reuse to a set of layers (a fixed schedule,
-  e.g. every other block);
-* ``threshold=inf`` accepts any drift without computing it, so the decision
-  needs no read of device memory and the step stays asynchronous. A zero-norm
-  ``hidden_in`` (for which the reference computes no drift and recomputes the
-  layer) is then reused too.
+How it runs here:
+
+* both sums of squares come from one HIP reduction over the two tensors
+  (``si_reuse_drift``); the host reads the two floats and finishes the ratio,
+  so a gated layer costs one small device read;
+* the reused output is one HIP pass (``si_reuse_apply``) instead of a
+  subtraction and an addition over the whole hidden state;
+* ``threshold=inf`` accepts every layer that has a record of the right shape
+  without computing the drift: no device read at all, and a denoising loop
+  stays asynchronous; ``reusable_layers`` limits reuse to a fixed set of
+  layers (e.g. every other block).
 """
 
 from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from typing import Any, Dict, FrozenSet, Optional, Set, Tuple
+from typing import Any, Dict, FrozenSet, List, Optional
 
 import torch
+
+from .. import _native
 
 
 @dataclass(frozen=True)
 class StepReuseConfig:
-    """step_reuse.py:18-33, plus ``reusable_layers`` (None = every layer)."""
+    """The reference's knobs (``enabled``, ``threshold``, ``warmup_steps``)
+    plus ``reusable_layers`` (None: every layer may be reused)."""
 
     enabled: bool = False
     threshold: float = 0.1
     warmup_steps: int = 1
     reusable_layers: Optional[FrozenSet[int]] = None
 
-    def validate(self) -> None:
+    def __post_init__(self) -> None:
         if self.threshold < 0:
             raise ValueError(f"step reuse threshold must be >= 0, got {self.threshold}")
         if self.warmup_steps < 0:
             raise ValueError(f"step reuse warmup_steps must be >= 0, got {self.warmup_steps}")
-
-    def __post_init__(self) -> None:
         if self.reusable_layers is not None:
-            object.__setattr__(self, "reusable_layers", frozenset(int(i) for i in self.reusable_layers))
-        self.validate()
+            object.__setattr__(self, "reusable_layers",
+                               frozenset(int(i) for i in self.reusable_layers))
+
+    def allows(self, layer: int, step_id: int) -> bool:
+        return (self.enabled and step_id >= self.warmup_steps
+                and (self.reusable_layers is None or layer in self.reusable_layers))
 
 
 @dataclass
-class LayerReuseEntry:
-    """step_reuse.py:36-43; ``k``/``v`` are None when the layer's KV lives
-    packed in ``packed_kv``."""
+class LayerRecord:
+    """What one computation of a layer leaves for the next steps."""
 
     hidden_in: torch.Tensor
     hidden_out: torch.Tensor
-    k: Optional[torch.Tensor] = None
-    v: Optional[torch.Tensor] = None
     packed_kv: Any = None
 
 
 @dataclass
+class _StepLog:
+    reused: List[int] = field(default_factory=list)
+    computed: List[int] = field(default_factory=list)
+    drifts: Dict[int, float] = field(default_factory=dict)
+
+
+def _round_to(x: float, dtype: torch.dtype) -> float:
+    """An fp32 value rounded to ``dtype`` (round to nearest even), as float."""
+    return float(torch.tensor(x, dtype=torch.float32).to(dtype).float())
+
+
 class StepReuseState:
-    """step_reuse.py:46-134."""
+    """Per-layer records across denoising steps and the log of the last step."""
 
-    entries: Dict[int, LayerReuseEntry] = field(default_factory=dict)
-    last_attention: Optional[torch.Tensor] = None
-    last_reused_layers: Set[int] = field(default_factory=set)
-    last_computed_layers: Set[int] = field(default_factory=set)
-    last_drifts: Dict[int, float] = field(default_factory=dict)
-    attention_reused: bool = False
+    def __init__(self) -> None:
+        self.records: Dict[int, LayerRecord] = {}
+        self._log = _StepLog()
+        self._scratch: Dict[torch.device, torch.Tensor] = {}
 
-    def reset(self) -> None:
-        self.entries.clear()
-        self.last_attention = None
-        self.last_reused_layers.clear()
-        self.last_computed_layers.clear()
-        self.last_drifts.clear()
-        self.attention_reused = False
+    def clear(self) -> None:
+        self.records.clear()
+        self._log = _StepLog()
 
-    def begin_step(self) -> None:
-        self.last_reused_layers = set()
-        self.last_computed_layers = set()
-        self.last_drifts = {}
-        self.attention_reused = False
+    def new_step(self) -> None:
+        self._log = _StepLog()
 
-    def drift(self, layer_id: int, hidden: torch.Tensor) -> Optional[float]:
-        """||hidden - hidden_in|| / ||hidden_in|| (step_reuse.py:71-80); None
-        without an entry of the same shape or for a zero-norm ``hidden_in``."""
-        entry = self.entries.get(layer_id)
-        if entry is None or entry.hidden_in.shape != hidden.shape:
+    # ------------------------------------------------------------- the gate
+    def relative_drift(self, record: LayerRecord, hidden: torch.Tensor) -> Optional[float]:
+        """``||hidden - hidden_in|| / ||hidden_in||`` in the hidden dtype's
+        arithmetic; None when ``hidden_in`` is all zeros (a NaN drift, from
+        non-finite states, never passes the gate)."""
+        _native.require_device(hidden, "StepReuseState.relative_drift")
+        a = hidden.contiguous()
+        b = record.hidden_in.contiguous()
+        dev = a.device
+        ws_bytes = _native.size_query("si_reuse_drift_workspace_bytes", a.numel())
+        buf = self._scratch.get(dev)
+        if buf is None or buf.numel() < ws_bytes + 8:
+            buf = torch.empty(ws_bytes + 8, dtype=torch.uint8, device=dev)
+            self._scratch[dev] = buf
+        sums = buf[ws_bytes:ws_bytes + 8].view(torch.float32)
+        _native.call("si_reuse_drift", a.data_ptr(), b.data_ptr(), _native.dtype_code(a.dtype),
+                     a.numel(), sums.data_ptr(), buf.data_ptr(), ws_bytes, _native.stream(dev))
+        s_diff, s_in = (float(x) for x in sums.cpu().tolist())
+        dt = a.dtype
+        denom = _round_to(math.sqrt(s_in), dt) if s_in >= 0.0 else float("nan")
+        if denom <= 0.0:
             return None
-        denom = entry.hidden_in.norm()
-        if float(denom) <= 0.0:
-            return None
-        return float((hidden - entry.hidden_in).norm() / denom)
+        return _round_to(_round_to(math.sqrt(s_diff), dt) / denom, dt)
 
-    def should_reuse(self, layer_id: int, hidden: torch.Tensor, step_id: int,
-                     config: StepReuseConfig) -> Tuple[bool, Optional[float]]:
-        """step_reuse.py:82-95."""
-        if not config.enabled or step_id < config.warmup_steps:
-            return False, None
-        if config.reusable_layers is not None and layer_id not in config.reusable_layers:
-            return False, None
+    def gate(self, layer: int, hidden: torch.Tensor, step_id: int,
+             config: StepReuseConfig) -> Optional[LayerRecord]:
+        """The record to reuse for ``layer`` this step, or None (compute it)."""
+        if not config.allows(layer, step_id):
+            return None
+        record = self.records.get(layer)
+        if record is None or record.hidden_in.shape != hidden.shape:
+            self.records.pop(layer, None)
+            return None
         if math.isinf(config.threshold):
-            entry = self.entries.get(layer_id)
-            if entry is None or entry.hidden_in.shape != hidden.shape:
-                self.entries.pop(layer_id, None)
-                return False, None
-            return True, None
-        drift = self.drift(layer_id, hidden)
+            return record
+        drift = self.relative_drift(record, hidden)
         if drift is None:
-            self.entries.pop(layer_id, None)
-            return False, None
-        return drift <= config.threshold, drift
+            self.records.pop(layer, None)
+            return None
+        self._log.drifts[layer] = drift
+        return record if drift <= config.threshold else None
 
-    def record(self, layer_id: int, hidden_in: torch.Tensor, hidden_out: torch.Tensor,
-               k: Optional[torch.Tensor] = None, v: Optional[torch.Tensor] = None,
-               packed_kv: Any = None) -> None:
-        """step_reuse.py:97-111. The tensors are kept, not copied: callers
-        must not modify them in place afterwards."""
-        self.entries[layer_id] = LayerReuseEntry(
-            hidden_in=hidden_in.detach(), hidden_out=hidden_out.detach(),
-            k=None if k is None else k.detach(), v=None if v is None else v.detach(),
-            packed_kv=packed_kv)
+    # ------------------------------------------------------ reuse and record
+    def reuse(self, layer: int, record: LayerRecord, hidden: torch.Tensor) -> torch.Tensor:
+        """The reused layer's output ``hidden_out + (hidden - hidden_in)``."""
+        _native.require_device(hidden, "StepReuseState.reuse")
+        h = hidden.contiguous()
+        hin = record.hidden_in.contiguous()
+        hout = record.hidden_out.contiguous()
+        out = torch.empty_like(h)
+        _native.call("si_reuse_apply", h.data_ptr(), hin.data_ptr(), hout.data_ptr(),
+                     _native.dtype_code(h.dtype), h.numel(), out.data_ptr(),
+                     _native.stream(h.device))
+        self._log.reused.append(layer)
+        return out.view(hidden.shape)
 
+    def keep(self, layer: int, hidden_in: torch.Tensor, hidden_out: torch.Tensor,
+             packed_kv: Any = None) -> None:
+        """Record a computed layer (the tensors are held, not copied)."""
+        self.records[layer] = LayerRecord(hidden_in.detach(), hidden_out.detach(), packed_kv)
+        self._log.computed.append(layer)
+
+    # --------------------------------------------------------------- stats
     def stats(self) -> Dict[str, Any]:
-        """step_reuse.py:113-125."""
-        reused = sorted(self.last_reused_layers)
-        computed = sorted(self.last_computed_layers)
-        total = len(reused) + len(computed)
-        return {
-            "reused_layers": reused,
-            "computed_layers": computed,
-            "reused_ratio": (len(reused) / total) if total else 0.0,
-            "drifts": dict(self.last_drifts),
-            "attention_reused": self.attention_reused,
-        }
+        """The last step's outcome, under the keys of the reference's
+        StepReuseState.stats (execution/step_reuse.py:113-125)."""
+        reused = sorted(self._log.reused)
+        computed = sorted(self._log.computed)
+        n = len(reused) + len(computed)
+        return {"reused_layers": reused, "computed_layers": computed,
+                "reused_ratio": len(reused) / n if n else 0.0,
+                "drifts": dict(self._log.drifts), "attention_reused": bool(reused)}

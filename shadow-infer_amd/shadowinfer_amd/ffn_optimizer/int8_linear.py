@@ -18,7 +18,7 @@ raises.
 from __future__ import annotations
 
 import logging
-from typing import Dict, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -31,39 +31,60 @@ _ACT_SCALE_EPS = 1e-8
 _WEIGHT_SCALE_EPS = 1e-8
 
 
+def _checked_layout(qweight_nk: torch.Tensor, weight_scale: torch.Tensor,
+                    bias: Optional[torch.Tensor], in_features: int, out_features: int) -> None:
+    """The constructor's contract (int8_linear.py:37-52), on the [N, K] weight:
+    ValueError for a non-int8 or misshapen weight, scale or bias."""
+    if qweight_nk.dtype != torch.int8:
+        raise ValueError(f"qweight must be int8, got {qweight_nk.dtype}")
+    if tuple(qweight_nk.shape) != (out_features, in_features):
+        raise ValueError(f"qweight of shape {tuple(qweight_nk.t().shape)} does not match "
+                         f"(in_features, out_features) = ({in_features}, {out_features})")
+    if weight_scale.dim() != 1 or weight_scale.numel() != out_features:
+        raise ValueError(f"weight_scale must be 1-D with {out_features} elements, got shape "
+                         f"{tuple(weight_scale.shape)}")
+    if bias is not None and bias.numel() != out_features:
+        raise ValueError(f"bias must have {out_features} elements, got {bias.numel()}")
+
+
 class INT8Linear(nn.Module):
-    """Linear layer with int8 weights, per-channel scales and dynamic activations."""
+    """Linear layer with int8 weights, per-channel scales and dynamic activations.
+
+    Constructed like the reference's (``qweight`` int8 ``[in_features,
+    out_features]``, ``weight_scale`` ``[out_features]``, optional ``bias``);
+    the weight is kept as its ``[out_features, in_features]`` transpose."""
 
     def __init__(self, qweight: torch.Tensor, weight_scale: torch.Tensor,
                  bias: Optional[torch.Tensor] = None, in_features: Optional[int] = None,
-                 out_features: Optional[int] = None, *,
-                 _qweight_nk: Optional[torch.Tensor] = None) -> None:
-        super().__init__()
-        if _qweight_nk is not None:
-            qweight = _qweight_nk.t()
+                 out_features: Optional[int] = None) -> None:
         if qweight.dim() != 2:
             raise ValueError(f"qweight must be 2-D, got shape {tuple(qweight.shape)}")
-        if qweight.dtype != torch.int8:
-            raise ValueError(f"qweight must be int8, got {qweight.dtype}")
-        in_features = in_features if in_features is not None else int(qweight.shape[0])
-        out_features = out_features if out_features is not None else int(qweight.shape[1])
-        if tuple(qweight.shape) != (in_features, out_features):
-            raise ValueError(
-                f"qweight shape {tuple(qweight.shape)} != ({in_features}, {out_features})")
-        if weight_scale.dim() != 1 or weight_scale.numel() != out_features:
-            raise ValueError(
-                f"weight_scale must have {out_features} elements, got {tuple(weight_scale.shape)}")
-        if bias is not None and bias.numel() != out_features:
-            raise ValueError(f"bias must have {out_features} elements")
-        self.in_features = int(in_features)
-        self.out_features = int(out_features)
-        nk = _qweight_nk if _qweight_nk is not None else qweight.t()
-        self.register_buffer("qweight_nk", nk.to(torch.int8).contiguous())
+        self._init_nk(qweight.t(), weight_scale, bias,
+                      int(qweight.shape[0]) if in_features is None else int(in_features),
+                      int(qweight.shape[1]) if out_features is None else int(out_features))
+
+    def _init_nk(self, qweight_nk: torch.Tensor, weight_scale: torch.Tensor,
+                 bias: Optional[torch.Tensor], in_features: int, out_features: int) -> None:
+        _checked_layout(qweight_nk, weight_scale, bias, in_features, out_features)
+        nn.Module.__init__(self)
+        self.in_features = in_features
+        self.out_features = out_features
+        self.register_buffer("qweight_nk", qweight_nk.contiguous())
         self.register_buffer("weight_scale", weight_scale.to(torch.float32).contiguous())
-        if bias is None:
-            self.register_buffer("bias", None)
-        else:
-            self.register_buffer("bias", bias.to(torch.float32).contiguous())
+        self.register_buffer("bias", None if bias is None
+                             else bias.to(torch.float32).reshape(-1).contiguous())
+
+    @classmethod
+    def from_quantized_nk(cls, qweight_nk: torch.Tensor, weight_scale: torch.Tensor,
+                          bias: Optional[torch.Tensor] = None) -> "INT8Linear":
+        """A layer over an int8 weight already in nn.Linear's ``[N, K]``
+        layout (no transpose copy)."""
+        if qweight_nk.dim() != 2:
+            raise ValueError(f"qweight_nk must be 2-D, got shape {tuple(qweight_nk.shape)}")
+        layer = cls.__new__(cls)
+        layer._init_nk(qweight_nk, weight_scale, bias, int(qweight_nk.shape[1]),
+                       int(qweight_nk.shape[0]))
+        return layer
 
     @classmethod
     def from_linear(cls, linear: nn.Linear) -> "INT8Linear":
@@ -78,8 +99,7 @@ class INT8Linear(nn.Module):
         _native.call("si_weight_quant_i8", weight.data_ptr(), N, K, q_nk.data_ptr(),
                      scale.data_ptr(), _native.stream(weight.device))
         bias = None if linear.bias is None else linear.bias.detach().to(torch.float32).clone()
-        return cls(qweight=None, weight_scale=scale, bias=bias, in_features=linear.in_features,
-                   out_features=linear.out_features, _qweight_nk=q_nk)
+        return cls.from_quantized_nk(q_nk, scale, bias)
 
     @property
     def qweight(self) -> torch.Tensor:
@@ -132,16 +152,14 @@ class INT8Linear(nn.Module):
         return out.reshape(*leading_shape, N)
 
     def memory_bytes(self) -> int:
-        total = self.qweight.numel() + self.weight_scale.numel() * 4
-        if self.bias is not None:
-            total += self.bias.numel() * 4
-        return int(total)
+        """Bytes held: the int8 weight, fp32 scales and fp32 bias
+        (int8_linear.py:128-132)."""
+        return sum(t.numel() * t.element_size()
+                   for t in (self.qweight_nk, self.weight_scale, self.bias) if t is not None)
 
     def dense_equivalent_bytes(self) -> int:
-        total = self.in_features * self.out_features * 4
-        if self.bias is not None:
-            total += self.out_features * 4
-        return int(total)
+        """Bytes of the fp32 layer it replaces (int8_linear.py:134-138)."""
+        return 4 * self.out_features * (self.in_features + (self.bias is not None))
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
@@ -149,8 +167,9 @@ class INT8Linear(nn.Module):
 
 
 def dequantized_weight(linear: INT8Linear) -> torch.Tensor:
-    """FP32 weight for diagnostics (int8_linear.py:146-148)."""
-    return linear.qweight.to(torch.float32) * linear.weight_scale.unsqueeze(0)
+    """The fp32 ``[in_features, out_features]`` weight ``q * s_w`` the layer
+    stands for, for diagnostics (int8_linear.py:146-148)."""
+    return (linear.qweight_nk.to(torch.float32) * linear.weight_scale[:, None]).t().contiguous()
 
 
 FFN_LINEAR_SUFFIXES = (
@@ -162,43 +181,58 @@ FFN_LINEAR_SUFFIXES = (
 )
 
 
+def _linear_slots(model: nn.Module, suffixes: Tuple[str, ...]):
+    """(owner module, attribute, child) for every submodule whose qualified
+    name ends with one of ``suffixes``: a pre-order walk of the module tree in
+    registration order, visiting a module registered twice only under its
+    first name (the order and the sharing rule of ``named_modules``)."""
+    seen = {id(model)}
+
+    def walk(prefix: str, owner: nn.Module):
+        for attr, child in owner.named_children():
+            if id(child) in seen:
+                continue
+            seen.add(id(child))
+            name = f"{prefix}.{attr}" if prefix else attr
+            if name.endswith(suffixes):
+                yield owner, attr, child
+            yield from walk(name, child)
+
+    yield from walk("", model)
+
+
 def quantize_ffn_modules(model: nn.Module, suffixes: tuple = FFN_LINEAR_SUFFIXES,
                          keep_fp32_reference: bool = False) -> Dict[str, object]:
-    """Replace matching FFN ``nn.Linear`` modules with INT8Linear
-    (int8_linear.py:160-208); idempotent."""
-    references = [] if keep_fp32_reference else None
-    modules = 0
-    weight_bytes = 0
-    dense_bytes = 0
-    fallback = False
-    for module_name, module in list(model.named_modules()):
-        if not any(module_name.endswith(suffix) for suffix in suffixes):
-            continue
-        if isinstance(module, INT8Linear):
-            modules += 1
-            weight_bytes += module.memory_bytes()
-            dense_bytes += module.dense_equivalent_bytes()
-            fallback = fallback or not module.using_int_mm
-            continue
-        if not isinstance(module, nn.Linear):
-            continue
-        parent_name, _, attribute = module_name.rpartition(".")
-        parent = model.get_submodule(parent_name) if parent_name else model
-        quantized = INT8Linear.from_linear(module)
-        if references is not None:
-            references.append((parent, attribute, module))
-        setattr(parent, attribute, quantized)
-        modules += 1
-        weight_bytes += quantized.memory_bytes()
-        dense_bytes += quantized.dense_equivalent_bytes()
-        fallback = fallback or not quantized.using_int_mm
-    if modules == 0:
+    """Swap the FFN projections of ``model`` (submodules whose qualified name
+    ends with one of ``suffixes``) for INT8Linear, in place
+    (int8_linear.py:160-208). nn.Linear layers are quantized; layers that are
+    already INT8Linear are counted as they are, so a second call changes
+    nothing. Returns ``{"supported": False}`` when nothing matches, else the
+    layer count, int8 and dense-equivalent weight bytes, whether any layer
+    lacks its int8 kernel (``fallback``), and with ``keep_fp32_reference``
+    the replaced layers as ``(owner, attribute, nn.Linear)`` under
+    ``_references``."""
+    layers: List[INT8Linear] = []
+    replaced: List[tuple] = []
+    for owner, attr, child in list(_linear_slots(model, tuple(suffixes))):
+        if isinstance(child, INT8Linear):
+            layers.append(child)
+        elif isinstance(child, nn.Linear):
+            layer = INT8Linear.from_linear(child)
+            setattr(owner, attr, layer)
+            layers.append(layer)
+            replaced.append((owner, attr, child))
+    if not layers:
         return {"supported": False}
-    stats: Dict[str, object] = {"supported": True, "modules": modules,
-                                "weight_bytes": weight_bytes, "dense_bytes": dense_bytes,
-                                "fallback": fallback}
-    if references:
-        stats["_references"] = references
+    stats: Dict[str, object] = {
+        "supported": True,
+        "modules": len(layers),
+        "weight_bytes": sum(layer.memory_bytes() for layer in layers),
+        "dense_bytes": sum(layer.dense_equivalent_bytes() for layer in layers),
+        "fallback": not all(layer.using_int_mm for layer in layers),
+    }
+    if keep_fp32_reference and replaced:
+        stats["_references"] = replaced
     return stats
 
 

@@ -1,11 +1,24 @@
 """Kernel-backend registry of the gfx950 data plane.
 
 Mirrors the reference's registry (shadowinfer/kernels/__init__.py:63-87,
-382-420): a status dict telling which kernels are active, a memoized,
-lock-guarded library load, and the internal int4 byte helpers used by the KV
-cache. Every kernel here is HIP; the status reports ``"hip"`` for a kernel
-whose library is loaded and ``"unavailable"`` otherwise (there is no CPU
-fallback to report).
+382-420; kernels/dispatcher.py:46-49): a status dict telling which kernels are
+active, a memoized, lock-guarded library load, and the internal int4 byte
+helpers used by the KV cache.
+
+``get_kernel_status()`` carries every key of the reference's status dict with
+the same types: ``cuda_available`` / ``cuda_extensions_loaded`` (booleans: a
+HIP device is visible / the HIP library is loaded), ``int8_kernel``,
+``int4_kernel``, ``sparse_gemm_kernel``, ``fused_attention_kernel`` (strings),
+``autotune_cache_entries`` (int) and ``force_cpu`` (bool, from
+``SHADOWINFER_FORCE_CPU_KERNELS=1``). A kernel this library provides reports
+``"hip"`` when the library is loaded and ``"unavailable"`` otherwise; the
+reference's sparse FFN GEMM is not part of this data plane and always reports
+``"unavailable"``, so callers that test for a native sparse GEMM take their
+dense path. There is no CPU fallback: with ``force_cpu`` set every kernel call
+raises RuntimeError. Tile choices come from closed-form models, so there is no
+autotuning cache (``autotune_cache_entries`` is 0). The build's own keys
+(``hip_*``, ``abi_version``, ``library``, ``load_error``, one entry per kernel
+family) follow.
 """
 
 from __future__ import annotations
@@ -15,21 +28,35 @@ from torch import Tensor
 
 from .. import _native
 
-__all__ = ["get_kernel_status", "_pack_int4", "_unpack_int4", "load_native"]
+__all__ = ["get_kernel_status", "_pack_int4", "_unpack_int4", "load_native", "force_cpu"]
 
+# kernel families of this library (the build's own status keys)
 _KERNELS = (
     "plan_scan_kernel",
     "kv_pack_kernel",
     "kv_unpack_kernel",
     "kv_reuse_kernel",
     "kv_compact_kernel",
-    "int8_kernel",
-    "int4_kernel",
     "int8_gemm_kernel",
-    "fused_attention_kernel",
     "kv_sensitivity_kernel",
     "admit_codes_kernel",
+    "paged_kv_kernel",
+    "step_row_kernel",
 )
+
+# keys of the reference's status dict (kernels/__init__.py:63-70) and whether
+# this library provides that kernel
+_REFERENCE_KERNELS = {
+    "int8_kernel": True,
+    "int4_kernel": True,
+    "sparse_gemm_kernel": False,
+    "fused_attention_kernel": True,
+}
+
+
+def force_cpu() -> bool:
+    """``SHADOWINFER_FORCE_CPU_KERNELS=1`` (reference kernels/dispatcher.py:46-49)."""
+    return _native.force_cpu()
 
 
 def load_native():
@@ -44,14 +71,23 @@ def get_kernel_status() -> dict:
         loaded, version = True, int(lib.si_abi_version())
     except RuntimeError:
         loaded, version = False, None
+    available = bool(torch.cuda.is_available())
     status = {
-        "hip_available": torch.cuda.is_available(),
+        "cuda_available": available,
+        "cuda_extensions_loaded": loaded,
+    }
+    for name, provided in _REFERENCE_KERNELS.items():
+        status[name] = "hip" if (loaded and provided) else "unavailable"
+    status["autotune_cache_entries"] = 0
+    status["force_cpu"] = force_cpu()
+    status.update({
+        "hip_available": available,
         "hip_extensions_loaded": loaded,
         "abi_version": version,
         "library": _native.LIB_PATH,
         "load_error": _native.load_error(),
         "cpu_fallback": False,
-    }
+    })
     for name in _KERNELS:
         status[name] = "hip" if loaded else "unavailable"
     return status

@@ -28,6 +28,7 @@ import numpy as np
 import torch
 
 from .. import _native
+from ._masks import token_head_mask
 from .precision_plan import EVICTED, PRECISION_ORDER, DeviceGrouping, PrecisionPlan
 
 _PREC_INDEX = {name: i for i, name in enumerate(PRECISION_ORDER)}
@@ -303,7 +304,7 @@ class PackedKVCache:
         else:
             if not token_head_set or not self._buckets:
                 return 0
-            mask = self._entry_mask(token_head_set.__iter__())
+            mask = self._entry_mask(token_head_set, is_dict=False)
             if mask is None:
                 return 0
         old = self._grouping
@@ -337,21 +338,12 @@ class PackedKVCache:
         self._view = None
         return removed
 
-    def _entry_mask(self, items) -> Optional[torch.Tensor]:
-        """uint8 [S*H] host mask of the (t, h) pairs that are in range."""
-        S, H = self.seq_len, self.num_heads
-        mask = np.zeros(S * H, dtype=np.uint8)
-        hit = False
-        for item in items:
-            try:
-                t, h = item
-                t, h = int(t), int(h)
-            except (TypeError, ValueError):
-                continue
-            if 0 <= t < S and 0 <= h < H:
-                mask[t * H + h] = 1
-                hit = True
-        return torch.from_numpy(mask) if hit else None
+    def _entry_mask(self, items, is_dict: bool) -> Optional[torch.Tensor]:
+        """uint8 [S*H] host mask of the in-range (t, h) pairs of the
+        reference's set (or, with ``is_dict``, of the dict's truthy keys),
+        built in one pass; None when no pair is in range."""
+        mask = token_head_mask(items, self.seq_len, self.num_heads, is_dict=is_dict)
+        return None if mask is None else torch.from_numpy(mask)
 
     def _precision_for(self, token_idx: int, head_idx: int) -> str:
         """packed_kv_cache.py:742-751: precision of an entry, EVICTED if absent."""
@@ -398,7 +390,7 @@ class PackedKVCache:
                 raise ValueError(f"reuse mask tensor must be [S, H], got {tuple(reuse_mask.shape)}")
             mask = reuse_mask.reshape(-1).to(device=dev, dtype=torch.uint8).contiguous()
         else:
-            host = self._entry_mask(k for k, flag in reuse_mask.items() if flag)
+            host = self._entry_mask(reuse_mask, is_dict=True)
             if host is None:
                 return stats if return_stats else None
             mask = host.to(dev)

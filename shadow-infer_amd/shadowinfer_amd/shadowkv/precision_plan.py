@@ -18,8 +18,10 @@ from __future__ import annotations
 
 import hashlib
 import struct
+from itertools import chain
 from typing import Any, Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from .. import _native
@@ -30,38 +32,85 @@ PRECISION_CODES: Dict[str, int] = {"fp32": 0, "fp16": 1, "int8": 2, "int4": 3, E
 CODE_PRECISIONS: Dict[int, str] = {code: name for name, code in PRECISION_CODES.items()}
 
 
+_FP16 = PRECISION_CODES["fp16"]
+_NAME_OF_CODE = np.array([CODE_PRECISIONS[c] for c in range(5)], dtype=object)
+
+
+def _index_in(key: Any, n: int) -> Optional[int]:
+    """The integer in [0, n) that ``key`` equals as a dict key (3, 3.0,
+    True, numpy integers), or None."""
+    try:
+        i = int(key)
+    except (TypeError, ValueError, OverflowError):
+        return None
+    return i if 0 <= i < n and i == key else None
+
+
+def _code_of(raw: Any, strict: bool) -> int:
+    name = raw.lower() if isinstance(raw, str) else raw
+    code = PRECISION_CODES.get(name) if isinstance(name, str) else None
+    if code is None:
+        if strict:
+            raise ValueError(f"Unsupported precision: {raw}")
+        return _FP16
+    return code
+
+
 def map_to_codes(precision_map: Dict[int, Dict[int, str]], seq_len: int, num_heads: int,
                  strict: bool = True, device: Any = "cpu") -> torch.Tensor:
-    """precision_plan.py:30-55: ``int8 [seq, heads]``; missing -> fp16; unknown
-    names raise ValueError when ``strict``, else become fp16."""
-    rows: List[List[int]] = []
-    for token_idx in range(seq_len):
-        token_map = precision_map.get(token_idx, {})
-        row: List[int] = []
-        for head_idx in range(num_heads):
-            raw = token_map.get(head_idx, "fp16")
-            precision = raw.lower() if isinstance(raw, str) else raw
-            if precision not in PRECISION_CODES:
-                if strict:
-                    raise ValueError(f"Unsupported precision: {raw}")
-                precision = "fp16"
-            row.append(PRECISION_CODES[precision])
-        rows.append(row)
-    return torch.tensor(rows, dtype=torch.int8, device=device).reshape(seq_len, num_heads)
+    """``int8 [seq_len, num_heads]`` codes of a ``token -> head -> name`` map
+    (precision_plan.py:30-55): entries the map does not name are fp16, names
+    are case-insensitive, an unknown name raises ValueError when ``strict`` and
+    is fp16 otherwise; keys outside the grid are ignored.
+
+    Only the entries the map holds are visited (a sparse map costs its size,
+    not seq_len * num_heads); the rest of the matrix is filled at once."""
+    codes = np.full((seq_len, num_heads), _FP16, dtype=np.int8)
+    rows = sorted(((t, row) for t, row in ((_index_in(k, seq_len), r)
+                                          for k, r in precision_map.items()) if t is not None),
+                  key=lambda tr: tr[0])
+    for t, row in rows:
+        named = [(h, raw) for h, raw in ((_index_in(k, num_heads), r) for k, r in row.items())
+                 if h is not None]
+        named.sort(key=lambda hr: hr[0])   # unknown names raise in (token, head) order
+        if named:
+            heads, raws = zip(*named)
+            codes[t, list(heads)] = [_code_of(r, strict) for r in raws]
+    return torch.from_numpy(codes).to(device)
 
 
 def codes_to_map(codes: torch.Tensor) -> Dict[int, Dict[int, str]]:
-    """precision_plan.py:58-69."""
-    values = codes.detach().to("cpu").to(torch.int64).tolist()
-    precision_map: Dict[int, Dict[int, str]] = {}
-    for token_idx, row in enumerate(values):
-        token_map: Dict[int, str] = {}
-        for head_idx, code in enumerate(row):
-            if code not in CODE_PRECISIONS:
-                raise ValueError(f"Unsupported precision code: {code}")
-            token_map[head_idx] = CODE_PRECISIONS[code]
-        precision_map[token_idx] = token_map
-    return precision_map
+    """``token -> head -> name`` map of an ``[S, H]`` code matrix
+    (precision_plan.py:58-69); a code outside 0..4 raises ValueError."""
+    values = codes.detach().to("cpu").to(torch.int64).numpy()
+    bad = (values < 0) | (values > 4)
+    if bad.any():
+        raise ValueError(f"Unsupported precision code: {int(values[bad][0])}")
+    names = _NAME_OF_CODE[values]
+    return {t: dict(enumerate(row)) for t, row in enumerate(names.tolist())}
+
+
+def _reuse_entries(reuse_mask: Optional[Dict[Tuple[int, int], bool]], seq_len: int,
+                   num_heads: int) -> List[Tuple[int, int]]:
+    """Sorted ``(int(t), int(h))`` of the truthy keys inside the grid
+    (precision_plan.py:154-163; repeats kept, fractions truncated by int()).
+    Numeric keys go through numpy in one pass; other keys take the
+    element-wise rule (which raises where the reference's unpacking does)."""
+    if not reuse_mask:
+        return []
+    n = len(reuse_mask)
+    try:
+        tk = np.fromiter(chain.from_iterable(reuse_mask.keys()), dtype=np.float64,
+                         count=2 * n).reshape(n, 2)
+        flag = np.fromiter(reuse_mask.values(), dtype=bool, count=n)
+    except (TypeError, ValueError):
+        out = sorted((int(t), int(h)) for (t, h), f in reuse_mask.items()
+                     if f and 0 <= t < seq_len and 0 <= h < num_heads)
+        return out
+    t, h = tk[:, 0], tk[:, 1]
+    keep = flag & (t >= 0) & (t < seq_len) & (h >= 0) & (h < num_heads)
+    flat = np.sort(t[keep].astype(np.int64) * num_heads + h[keep].astype(np.int64))
+    return list(zip((flat // num_heads).tolist(), (flat % num_heads).tolist()))
 
 
 class DeviceGrouping:
@@ -184,13 +233,9 @@ class PrecisionPlan:
         device = torch.device(device)
         codes = codes.detach().to(device=device, dtype=torch.int8).contiguous()
 
-        reuse_entries: List[Tuple[int, int]] = []
-        if reuse_mask:
-            reuse_entries = sorted(
-                (int(t), int(h)) for (t, h), flag in reuse_mask.items()
-                if flag and 0 <= t < seq_len and 0 <= h < num_heads)
-        reuse_flat = torch.tensor([h * seq_len + t for t, h in reuse_entries], dtype=torch.long,
-                                  device=device)
+        reuse_entries = _reuse_entries(reuse_mask, seq_len, num_heads)
+        pairs = np.array(reuse_entries, dtype=np.int64).reshape(-1, 2)
+        reuse_flat = torch.from_numpy(pairs[:, 1] * seq_len + pairs[:, 0]).to(device)
 
         if device.type == "cpu":
             return cls._from_codes_host(codes, reuse_entries, reuse_flat)
@@ -212,23 +257,29 @@ class PrecisionPlan:
 
     @classmethod
     def _from_codes_host(cls, codes: torch.Tensor, reuse_entries, reuse_flat) -> "PrecisionPlan":
-        """Host metadata for a CPU plan (precision_plan.py:132-151)."""
-        seq_len, num_heads = int(codes.shape[0]), int(codes.shape[1])
-        flat = codes.reshape(-1).to(torch.int64)
-        groups: Dict[str, List[Tuple[int, int]]] = {p: [] for p in PRECISION_ORDER}
+        """Host metadata of a CPU plan (the grouping of precision_plan.py:132-151):
+        one stable argsort of the flat codes puts each code's entries together
+        in token-major order; codes outside 0..4 belong to no group."""
+        S, H = int(codes.shape[0]), int(codes.shape[1])
+        flat = codes.reshape(-1).numpy().astype(np.int64)
+        order = np.argsort(flat, kind="stable")
+        counts = np.bincount(flat[(flat >= 0) & (flat <= 4)], minlength=5)
+        first = int(np.count_nonzero(flat < 0))
+        bounds = first + np.concatenate(([0], np.cumsum(counts)))
+        groups: Dict[str, List[Tuple[int, int]]] = {}
         flat_indices: Dict[str, torch.Tensor] = {}
         evicted: List[Tuple[int, int]] = []
-        for code, precision in CODE_PRECISIONS.items():
-            selected = (flat == code).nonzero(as_tuple=False).reshape(-1)
-            token_idx = torch.div(selected, num_heads, rounding_mode="floor")
-            head_idx = torch.remainder(selected, num_heads)
-            pairs = list(zip(token_idx.tolist(), head_idx.tolist()))
-            if precision == EVICTED:
+        for code in range(5):
+            e = order[bounds[code]: bounds[code + 1]]
+            t, h = e // H, e % H
+            pairs = list(zip(t.tolist(), h.tolist()))
+            if code == PRECISION_CODES[EVICTED]:
                 evicted = pairs
             else:
-                groups[precision] = pairs
-                flat_indices[precision] = (head_idx * seq_len + token_idx).to(torch.long)
-        return cls(seq_len, num_heads, codes, flat_indices, reuse_entries, reuse_flat,
+                name = CODE_PRECISIONS[code]
+                groups[name] = pairs
+                flat_indices[name] = torch.from_numpy(h * S + t)
+        return cls(S, H, codes, flat_indices, reuse_entries, reuse_flat,
                    groups=groups, evicted_entries=evicted)
 
     # ------------------------------------------------------------- lazy views

@@ -111,29 +111,51 @@ class Quantizer:
 
     @staticmethod
     def dequantize_int4(quantized: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
-        """``(quantized.float() * scale).reshape(..., -1)`` (quantization.py:199-219)."""
+        """``(quantized.float() * scale).reshape(*quantized.shape[:-2], -1)``
+        (quantization.py:199-219)."""
         out = Quantizer._dequant(quantized, scale, per_group=True)
         return out.reshape(*quantized.shape[:-2], -1)
 
     @staticmethod
     def _dequant(q: torch.Tensor, scale: torch.Tensor, per_group: bool) -> torch.Tensor:
+        """``q.float() * scale`` with any scale that broadcasts against ``q``
+        (quantization.py:180-219): per-row ``[..., 1]`` and per-group scales,
+        a per-tensor or 0-d scale (what quantize_* return for an empty
+        tensor), or one scale per element. Result fp32 of the broadcast shape,
+        each element ``float(q) * float(scale)`` (one fp32 multiply, as torch
+        computes it). Codes are int8; scales fp32/fp16/bf16 (float64 scales,
+        which torch would promote to a float64 result, raise TypeError)."""
+        if not torch.is_tensor(scale):
+            scale = torch.tensor(float(scale), dtype=torch.float32, device=q.device)
+        if q.dtype != torch.int8:
+            raise ValueError(f"dequantize expects int8 codes, got {q.dtype}")
+        if scale.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise TypeError(f"dequantize supports fp32/fp16/bf16 scales, got {scale.dtype}")
+        if scale.device != q.device:
+            if scale.dim() != 0:
+                raise ValueError(f"scale on {scale.device} but codes on {q.device}")
+            scale = scale.to(q.device)  # a 0-d tensor broadcasts across devices in torch
+        shape = tuple(torch.broadcast_shapes(q.shape, scale.shape))
+        n = 1
+        for d in shape:
+            n *= d
+        if n == 0:
+            return torch.empty(shape, dtype=torch.float32, device=q.device)
         _native.require_device(q, "Quantizer.dequantize")
-        expected = q.shape[:-1] + (1,)
-        if (q.dtype != torch.int8 or tuple(scale.shape) != tuple(expected)
-                or scale.dtype not in (torch.float32, torch.float16, torch.bfloat16)
-                or scale.device != q.device):
-            raise ValueError(
-                f"dequantize expects int8 codes [..., g] and scales [..., 1] on the same device "
-                f"(got {tuple(q.shape)} {q.dtype}, {tuple(scale.shape)} {scale.dtype})")
-        qc = q.contiguous()
-        sc = scale.contiguous()
-        D = qc.shape[-1]
-        rows = qc.numel() // D if D else 0
-        out = torch.empty(qc.shape, dtype=torch.float32, device=qc.device)
-        if rows:
-            _native.call("si_dequant_rows", qc.data_ptr(), sc.data_ptr(),
-                         _native.dtype_code(sc.dtype), rows, D, D, out.data_ptr(),
-                         _native.stream(qc.device))
+        D = shape[-1] if shape else 1
+        rows = n // D
+        qc = (q.expand(shape) if tuple(q.shape) != shape else q).contiguous().reshape(rows, D)
+        if scale.dim() == 0 or scale.shape[-1] == 1:
+            # constant along the last dim: one scale per row
+            sc = scale.reshape(scale.shape[:-1] if scale.dim() else ())
+            sc = sc.expand(shape[:-1]).contiguous().reshape(rows)
+            group = D
+        else:
+            sc = scale.expand(shape).contiguous().reshape(rows, D)
+            group = 1
+        out = torch.empty(shape, dtype=torch.float32, device=q.device)
+        _native.call("si_dequant_rows", qc.data_ptr(), sc.data_ptr(), _native.dtype_code(sc.dtype),
+                     rows, D, group, out.data_ptr(), _native.stream(q.device))
         return out
 
     @staticmethod

@@ -20,6 +20,7 @@ import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 from scipy.special import expit
 
 from helpers import DT, assert_cache_equal, to_np
@@ -64,6 +65,11 @@ def f32(x, dt):
 
 
 # ----------------------------------------------------------------- CPU pins
+def _t16(a):
+    """uint16 bf16 bit patterns -> CPU bf16 tensor."""
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
 def test_rmsnorm_ref_closed_form_and_invariants():
     # constant row c: y = c / sqrt(c^2 + eps) (catches eps outside the sqrt)
     for c, eps in ((1e-3, 1e-5), (2.0, 1e-6), (-0.5, 0.0)):
@@ -79,14 +85,25 @@ def test_rmsnorm_ref_closed_form_and_invariants():
     np.testing.assert_allclose(np.sqrt((y1.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-6)
     np.testing.assert_array_equal(R.rmsnorm(4 * x, O.F32, w, 0.0), y)
     np.testing.assert_array_equal(R.rmsnorm(x, O.F32, 2 * w, 0.0), 2 * y)
-    # bf16: the fp32 result rounded once (RNE) to bf16
-    xb = O.from_f32(x, O.BF16)
-    yb = R.rmsnorm(xb, O.BF16, O.from_f32(w, O.BF16), 1e-5)
-    xf = O.to_f32(xb, O.BF16).astype(np.float64)
-    wf = O.to_f32(O.from_f32(w, O.BF16), O.BF16).astype(np.float64)
-    want = torch.from_numpy((xf / np.sqrt((xf ** 2).mean(-1, keepdims=True) + 1e-5) * wf)
-                            .astype(np.float32)).to(torch.bfloat16)
-    np.testing.assert_array_equal(yb, to_np(want))
+
+
+@pytest.mark.parametrize("K", [64, 4096])
+def test_rmsnorm_ref_is_the_torch_op_chain(K):
+    """DiffusionLlamaRMSNorm.forward's ops run in CPU bf16 torch (a power-of-two
+    K, where torch's CPU mean and its GPU mean round alike) give the oracle's
+    bits on every row it does not flag; rounding once instead of per op would
+    differ on most rows."""
+    g = torch.Generator().manual_seed(K)
+    x = (torch.randn(384, K, generator=g) * 3).to(torch.bfloat16)
+    w = (torch.rand(K, generator=g) + 0.5).to(torch.bfloat16)
+    want = to_np(x / torch.sqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5) * w)
+    y, amb = R.rmsnorm(to_np(x), O.BF16, to_np(w), 1e-5, return_ambiguous=True)
+    assert amb.mean() < 0.05
+    np.testing.assert_array_equal(y[~amb], want[~amb])
+    once = O.from_f32((f32(to_np(x), O.BF16).astype(np.float64) / np.sqrt(
+        (f32(to_np(x), O.BF16).astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-5)
+        * f32(to_np(w), O.BF16)).astype(np.float32), O.BF16)
+    assert (once != want).any(-1).mean() > 0.5
 
 
 def test_rope_ref_rotation():
@@ -123,18 +140,89 @@ def test_rope_ref_rotation():
     assert abs(s1 - s2) < 1e-4 * max(1.0, abs(s1))
 
 
-def test_swiglu_ref_matches_library_silu():
-    rng = np.random.default_rng(2)
-    g = (rng.standard_normal((4, 40)) * 4).astype(np.float32)
-    u = rng.standard_normal((4, 40)).astype(np.float32)
-    gb, ub = O.from_f32(g, O.BF16), O.from_f32(u, O.BF16)
-    h = R.swiglu(np.concatenate([gb, ub], 1), O.BF16)
-    gf = O.to_f32(gb, O.BF16).astype(np.float64)
-    sg = O.to_f32(O.from_f32((gf * expit(gf)).astype(np.float32), O.BF16), O.BF16).astype(np.float64)
-    want = O.from_f32((sg * O.to_f32(ub, O.BF16)).astype(np.float32), O.BF16)
-    assert ulp_diff(h, want).max() <= 1
+def _rotate_half(t):
+    h = t.shape[-1] // 2
+    return torch.cat((-t[..., h:], t[..., :h]), dim=-1)
+
+
+def test_rope_ref_is_the_torch_op_chain():
+    """q * cos + rotate_half(q) * sin in CPU bf16 torch (diffusion_llama.py:288-292,
+    372-373): bit for bit (no reduction is involved)."""
+    B, S, H, D = 2, 40, 3, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = (torch.randn(B * S, 3 * H * D, generator=g) * 2).to(torch.bfloat16)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.outer(torch.arange(S, dtype=torch.float32), inv)
+    emb = torch.cat((emb, emb), -1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    x = qkv.view(B, S, 3, H, D)
+    rq, rk, rv = R.rope_split(to_np(qkv), O.BF16, to_np(cos), to_np(sin), B, S, H, D)
+    for j, got in ((0, rq), (1, rk)):
+        t = x[:, :, j].transpose(1, 2)
+        np.testing.assert_array_equal(got, to_np(t * cos + _rotate_half(t) * sin))
+    np.testing.assert_array_equal(rv, to_np(x[:, :, 2].transpose(1, 2)))
+
+
+def test_swiglu_ref_is_the_torch_op_chain():
+    """F.silu(gate) * up in CPU bf16 torch (diffusion_llama.py:333): equal on
+    every element the oracle does not flag, and a zero gate gives zero."""
+    g = torch.Generator().manual_seed(2)
+    gate = (torch.randn(64, 1024, generator=g) * 4).to(torch.bfloat16)
+    up = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    h, amb = R.swiglu(np.concatenate([to_np(gate), to_np(up)], 1), O.BF16, return_ambiguous=True)
+    want = to_np(F.silu(gate) * up)
+    assert amb.mean() < 0.01
+    np.testing.assert_array_equal(h[~amb], want[~amb])
+    gf = f32(to_np(gate), O.BF16).astype(np.float64)
+    assert ulp_diff(O.from_f32((gf * expit(gf)).astype(np.float32), O.BF16),
+                    to_np(F.silu(gate))).max() <= 1
     z = R.swiglu(np.zeros((1, 16), np.float32), O.F32)
     np.testing.assert_array_equal(z, 0.0)
+
+
+def _bf16_bits(x):
+    return O.from_f32(np.asarray(x, np.float32), O.BF16)
+
+
+def test_argmax_conf_ref_known_answers():
+    """softmax(logits).max(-1) in bf16 (block_decoding.py:146-147).
+    Row 0: logits 0 and 0.001 have probabilities that round to the same bf16
+    value, so the FIRST index wins although index 1 holds the larger logit.
+    Row 1: a NaN gives NaN and index 0. Row 2: +inf likewise. Row 3: -inf
+    entries have probability 0 and do not take part; the tie of the two 3.0
+    logits goes to the first."""
+    rows = [[0.0, 0.001, -3.0, -3.0], [0.0, float("nan"), 1.0, 2.0],
+            [0.0, 1.0, float("inf"), 2.0], [float("-inf"), 3.0, float("-inf"), 3.0]]
+    lg = _bf16_bits(rows)
+    tok, conf = R.argmax_conf(lg, O.BF16)
+    ref_p = torch.softmax(_t16(lg), -1)
+    rc, rt = ref_p.max(-1)
+    np.testing.assert_array_equal(tok, rt.numpy())
+    np.testing.assert_array_equal(conf, to_np(rc))
+    assert f32(lg, O.BF16)[0, 1] > f32(lg, O.BF16)[0, 0]
+    assert tok[0] == 0 and tok[1] == 0 and tok[2] == 0 and tok[3] == 1
+    assert np.isnan(f32(conf[1:3], O.BF16)).all()
+    assert f32(conf[3:], O.BF16)[0] == 0.5
+
+
+@pytest.mark.parametrize("dtype,V,scale", [(torch.bfloat16, 1000, 0.05), (torch.bfloat16, 32000, 1.0),
+                                           (torch.float32, 1000, 0.05)])
+def test_argmax_conf_ref_is_the_torch_op_chain(dtype, V, scale):
+    """torch.softmax(logits, -1).max(-1) in CPU torch on random logits equals
+    the oracle on every row it does not flag; the argmax of the logits (the
+    rule this replaces) differs from it on a sizeable share of bf16 rows."""
+    g = torch.Generator().manual_seed(V)
+    lg = (torch.randn(192, V, generator=g) * scale).to(dtype)
+    c, t = torch.softmax(lg, -1).max(-1)
+    rt, rc, amb = R.argmax_conf(to_np(lg), DT[dtype], return_ambiguous=True)
+    assert amb.mean() < 0.05
+    np.testing.assert_array_equal(rt[~amb], t.numpy()[~amb])
+    if dtype == torch.float32:
+        np.testing.assert_allclose(rc, to_np(c), rtol=2 * R.SUM_REL_ERR)
+    else:
+        np.testing.assert_array_equal(rc[~amb], to_np(c)[~amb])
+    if dtype == torch.bfloat16 and scale < 1:
+        assert (lg.float().argmax(-1).numpy() != rt).mean() > 0.02
 
 
 def _conf_row(conf, token, vocab):
@@ -155,11 +243,24 @@ def test_schedule_ref_known_answers():
     tok, conf = R.argmax_conf(logits, O.F32)
     np.testing.assert_array_equal(tok, np.array(toks))
     np.testing.assert_allclose(conf, np.array(confs), rtol=1e-5)
-    unmask, fb = R.schedule(conf, masked, 0.9)
+    unmask, fb = R.schedule(conf, masked, 0.9, O.F32)
     # row 0: both above 0.9; row 1: fallback, tie 0.6/0.6 -> smaller index;
     # row 2: nothing masked
     np.testing.assert_array_equal(unmask, [[1, 0, 1, 0], [0, 1, 0, 0], [0, 0, 0, 0]])
     np.testing.assert_array_equal(fb, [False, True, False])
+
+
+def test_schedule_ref_threshold_in_the_logits_dtype():
+    """A bf16 confidence of 0.8984375 (= bf16(0.9)) reaches the 0.9 threshold,
+    as torch's bf16 comparison with a Python float decides; 0.89453125 does not.
+    Two tied bf16 confidences fall back to the smaller position."""
+    conf = _bf16_bits([[0.8984375, 0.5], [0.89453125, 0.5], [0.25, 0.25]])
+    masked = np.ones((3, 2), bool)
+    unmask, fb = R.schedule(conf, masked, 0.9, O.BF16)
+    want = (_t16(conf) >= 0.9).numpy()
+    np.testing.assert_array_equal(unmask[0], want[0])
+    np.testing.assert_array_equal(unmask, [[1, 0], [1, 0], [1, 0]])
+    np.testing.assert_array_equal(fb, [False, True, True])
 
 
 # ------------------------------------------------------------------ GPU
@@ -168,28 +269,55 @@ def _need_lib():
     _native.load()
 
 
+def _assert_rows_equal(got, want, amb, dtype):
+    """Equal bits on every row the oracle does not flag (16-bit dtypes); fp32
+    rows keep the fp32 reduction-order error."""
+    if dtype == torch.float32:
+        np.testing.assert_allclose(got, want, rtol=4 * R.SUM_REL_ERR, atol=1e-30)
+        return
+    assert amb.mean() < 0.05
+    np.testing.assert_array_equal(got[~amb], want[~amb])
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("M,K", [(1, 8), (37, 256), (64, 4096), (5, 11008), (3, 16384)])
 def test_rmsnorm_kernel(dev, dtype, M, K):
+    """RMSNorm as the reference's op chain: against the oracle and against the
+    same torch ops on the GPU; with the residual add fused in front."""
     from shadowinfer_amd.execution import row_ops
     g = torch.Generator().manual_seed(M * 7 + K)
     x = (torch.randn(M, K, generator=g) * 3).to(dtype)
+    o = torch.randn(M, K, generator=g).to(dtype)
     w = (torch.rand(K, generator=g) + 0.5).to(dtype)
-    y, q, s = row_ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, want_y=True, want_q=True)
+    y, q, s, _ = row_ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, want_y=True, want_q=True)
     dt = DT[dtype]
-    assert_row_kernel_close(to_np(y), R.rmsnorm(to_np(x), dt, to_np(w), 1e-5), dtype)
+    want, amb = R.rmsnorm(to_np(x), dt, to_np(w), 1e-5, return_ambiguous=True)
+    _assert_rows_equal(to_np(y), want, amb, dtype)
+    xd, wd = x.to(dev), w.to(dev)
+    torch_y = xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-5) * wd
+    _assert_rows_equal(to_np(y), to_np(torch_y), amb, dtype)
     qr, sr = O.int8_act_quant(to_np(y), dt)      # fused quantization of the kernel's own y
     np.testing.assert_array_equal(to_np(q), qr)
     np.testing.assert_array_equal(to_np(s), sr)
-    _, q2, s2 = row_ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, want_y=False, want_q=True)
+    _, q2, s2, _ = row_ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, want_y=False, want_q=True)
     assert torch.equal(q2, q) and torch.equal(s2, s)
+    # residual add + RMSNorm: x1 = x + o in the dtype, then the same chain
+    y3, q3, s3, x1 = row_ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, want_q=True, residual=o.to(dev))
+    np.testing.assert_array_equal(to_np(x1), R.add(to_np(x), to_np(o), dt))
+    assert torch.equal(x1, xd + o.to(dev))
+    want3, amb3 = R.rmsnorm(to_np(x1), dt, to_np(w), 1e-5, return_ambiguous=True)
+    _assert_rows_equal(to_np(y3), want3, amb3, dtype)
+    qr3, sr3 = O.int8_act_quant(to_np(y3), dt)
+    np.testing.assert_array_equal(to_np(q3), qr3)
+    np.testing.assert_array_equal(to_np(s3), sr3)
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("B,S,H,D", [(1, 7, 3, 64), (2, 33, 4, 128), (1, 256, 32, 128)])
 def test_rope_kernel(dev, dtype, B, S, H, D):
+    """Bit-exact to the oracle and to q * cos + rotate_half(q) * sin on the GPU."""
     from shadowinfer_amd.execution import row_ops
     g = torch.Generator().manual_seed(S * H + D)
     qkv = torch.randn(B * S, 3 * H * D, generator=g).to(dtype)
@@ -200,22 +328,36 @@ def test_rope_kernel(dev, dtype, B, S, H, D):
     q, k, v = row_ops.rope_split(qkv.to(dev), cos.to(dev), sin.to(dev), B, S, H, D)
     dt = DT[dtype]
     rq, rk, rv = R.rope_split(to_np(qkv), dt, to_np(cos), to_np(sin), B, S, H, D)
-    for got, want in ((q, rq), (k, rk)):
-        assert_row_kernel_close(to_np(got), want, dtype)
+    np.testing.assert_array_equal(to_np(q), rq)
+    np.testing.assert_array_equal(to_np(k), rk)
     np.testing.assert_array_equal(to_np(v), rv)
+    x = qkv.to(dev).view(B, S, 3, H, D)
+    c, sn = cos.to(dev), sin.to(dev)
+    for j, got in ((0, q), (1, k)):
+        t = x[:, :, j].transpose(1, 2)
+        assert torch.equal(got, t * c + _rotate_half(t) * sn)
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("M,F", [(1, 8), (19, 512), (64, 11008), (2, 16384)])
 def test_swiglu_kernel(dev, dtype, M, F):
+    """h = silu(gate) * up bit for bit as torch computes it on the GPU
+    (F.silu then the product, both in the dtype); against the oracle on every
+    element it does not flag (its exp is correctly rounded, the device's expf
+    may be an ulp off)."""
     from shadowinfer_amd.execution import row_ops
     g = torch.Generator().manual_seed(M + F)
     gu = (torch.randn(M, 2 * F, generator=g) * 3).to(dtype)
+    gu[0, :8] = torch.tensor([0.0, -0.0, 80.0, -80.0, 100.0, -100.0, 1e-3, -1e-3]).to(dtype)
     h, q, s = row_ops.swiglu_quant(gu.to(dev), want_h=True)
     dt = DT[dtype]
-    # two roundings (silu, then the product): within 2 units in the last place
-    assert_row_kernel_close(to_np(h), R.swiglu(to_np(gu), dt), dtype, max_ulp=2)
+    gd = gu.to(dev)
+    torch_h = F.silu(gd[:, :F]) * gd[:, F:]
+    assert torch.equal(h, torch_h)
+    want, amb = R.swiglu(to_np(gu), dt, return_ambiguous=True)
+    assert amb.mean() < 0.01
+    np.testing.assert_array_equal(to_np(h)[~amb], want[~amb])
     qr, sr = O.int8_act_quant(to_np(h), dt)
     np.testing.assert_array_equal(to_np(q), qr)
     np.testing.assert_array_equal(to_np(s), sr)
@@ -224,24 +366,52 @@ def test_swiglu_kernel(dev, dtype, M, F):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("M,V", [(3, 1), (5, 7), (64, 32000), (2, 50001)])
-def test_argmax_conf_kernel(dev, dtype, M, V):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("M,V,scale", [(3, 1, 1.0), (5, 7, 1.0), (64, 32000, 0.05),
+                                       (64, 32000, 4.0), (2, 50001, 1.0), (33, 1000, 0.02)])
+def test_argmax_conf_kernel(dev, dtype, M, V, scale):
+    """softmax(logits).max(-1) in the logits' dtype: tokens and confidences
+    against torch's own softmax + max on the GPU and against the oracle, on
+    every row the oracle does not flag; rows with NaN / +inf / only -inf."""
     from shadowinfer_amd.execution import argmax_confidence
     g = torch.Generator().manual_seed(M * V)
-    logits = (torch.randn(M, V, generator=g) * 4).to(dtype)
+    logits = (torch.randn(M, V, generator=g) * scale).to(dtype)
     if V >= 7:
         logits[0, :] = 1.0                     # all tied: first index
         logits[1, 3] = logits[1, 5] = 1e4      # tie of two maxima
     tok, conf = argmax_confidence(logits.to(dev))
-    rt, rc = R.argmax_conf(to_np(logits), DT[dtype])
-    np.testing.assert_array_equal(tok.cpu().numpy(), rt)
-    np.testing.assert_allclose(conf.cpu().numpy(), rc, rtol=1e-5)
-    nan = torch.zeros(1, 9)
-    nan[0, 4] = float("nan")
-    nan[0, 6] = float("nan")
-    t2, c2 = argmax_confidence(nan.to(dev))
-    assert int(t2[0]) == 4 and math.isnan(float(c2[0]))
+    assert conf.dtype == dtype
+    rt, rc, amb = R.argmax_conf(to_np(logits), DT[dtype], return_ambiguous=True)
+    assert amb.mean() < 0.05
+    tc, tt = torch.softmax(logits.to(dev), dim=-1).max(dim=-1)
+    for want_t, want_c in ((rt, rc), (tt.cpu().numpy(), to_np(tc))):
+        np.testing.assert_array_equal(tok.cpu().numpy()[~amb], want_t[~amb])
+        if dtype == torch.float32:
+            np.testing.assert_allclose(to_np(conf), want_c, rtol=4 * R.SUM_REL_ERR)
+        else:
+            np.testing.assert_array_equal(to_np(conf)[~amb], want_c[~amb])
+    bad = torch.zeros(3, 9)
+    bad[0, 4] = bad[0, 6] = float("nan")
+    bad[1, 2] = float("inf")
+    bad[2, :] = float("-inf")
+    t2, c2 = argmax_confidence(bad.to(dtype).to(dev))
+    assert t2.tolist() == [0, 0, 0] and bool(torch.isnan(c2.float()).all())
+
+
+def _reference_schedule(logits, masked, threshold):
+    """block_decoding.py:144-165 as torch ops on the device (the reference's
+    op sequence; its boolean-index assignment written as a loop over rows)."""
+    probs = torch.softmax(logits, dim=-1)
+    confidences, tokens = probs.max(dim=-1)
+    above = masked & (confidences >= threshold)
+    needs_fallback = masked.any(dim=1) & ~above.any(dim=1)
+    fallback_positions = confidences.masked_fill(~masked, float("-inf")).argmax(dim=1)
+    fallback_unmask = torch.zeros_like(above)
+    for b in range(masked.shape[0]):
+        if bool(needs_fallback[b]):
+            fallback_unmask[b, fallback_positions[b]] = True
+    unmask = above | fallback_unmask
+    return unmask, tokens, confidences * (masked & ~unmask), needs_fallback
 
 
 @pytest.mark.gpu
@@ -257,24 +427,28 @@ def test_schedule_round_matches_reference_rule(dev):
     np.testing.assert_array_equal(d.unmask.cpu().numpy(), [[1, 0, 1, 0], [0, 1, 0, 0], [0, 0, 0, 0]])
     np.testing.assert_array_equal(d.progress_fallback.cpu().numpy(), [False, True, False])
     np.testing.assert_array_equal(d.tokens.cpu().numpy(), toks)
-    # random blocks against the per-element rule (reference tests/test_block_decoding.py:363-384)
-    for b, w, v in ((1, 1, 2), (2, 5, 4), (3, 8, 16), (4, 64, 1000)):
-        g = torch.Generator().manual_seed(b * 100 + w * 7 + v)
-        lg = torch.randn(b, w, v, generator=g)
-        mk = torch.rand(b, w, generator=g) < 0.6
-        for thr in (0.9, 0.3):
-            d = schedule_round(lg.to(dev), mk.to(dev), thr)
-            _, conf = R.argmax_conf(lg.numpy(), O.F32)
-            ru, rf = R.schedule(conf, mk.numpy(), thr)
-            np.testing.assert_array_equal(d.unmask.cpu().numpy(), ru)
-            np.testing.assert_array_equal(d.progress_fallback.cpu().numpy(), rf)
-            still = (mk & ~d.unmask.cpu()).numpy()
-            np.testing.assert_allclose(d.confidences.cpu().numpy()[still], conf[still], rtol=1e-5)
-            assert not d.confidences.cpu().numpy()[~still].any()
+    # random blocks, fp32 and bf16, against the reference's op sequence on the
+    # GPU and the oracle's per-element rule (reference tests/test_block_decoding.py:363-384)
+    for dtype in (torch.float32, torch.bfloat16):
+        for b, w, v, sc in ((1, 1, 2, 1.0), (2, 5, 4, 1.0), (3, 8, 16, 1.0), (4, 64, 1000, 1.0),
+                            (4, 256, 32000, 0.05), (2, 128, 64, 3.0)):
+            g = torch.Generator().manual_seed(b * 100 + w * 7 + v)
+            lg = (torch.randn(b, w, v, generator=g) * sc).to(dtype).to(dev)
+            mk = (torch.rand(b, w, generator=g) < 0.6).to(dev)
+            for thr in (0.9, 0.3, 0.2617):
+                d = schedule_round(lg, mk, thr)
+                ru, rt, rc, rf = _reference_schedule(lg, mk, thr)
+                assert torch.equal(d.unmask, ru) and torch.equal(d.progress_fallback, rf)
+                assert torch.equal(d.tokens[d.unmask], rt[d.unmask])
+                assert torch.equal(d.confidences, rc)
+                _, conf = R.argmax_conf(to_np(lg), DT[dtype])
+                ou, of = R.schedule(conf, mk.cpu().numpy(), thr, DT[dtype])
+                np.testing.assert_array_equal(d.unmask.cpu().numpy(), ou)
+                np.testing.assert_array_equal(d.progress_fallback.cpu().numpy(), of)
     with pytest.raises(ValueError):
-        schedule_round(lg.to(dev)[0], mk.to(dev), 0.9)
+        schedule_round(lg[0], mk, 0.9)
     with pytest.raises(ValueError):
-        schedule_round(lg.to(dev), mk.to(dev)[:, :1], 0.9)
+        schedule_round(lg, mk[:, :1], 0.9)
 
 
 @pytest.mark.gpu
@@ -311,18 +485,12 @@ def _plans(dev, S, H, L, seed=5):
     return codes, [PrecisionPlan.from_codes(torch.from_numpy(c).to(dev)) for c in codes]
 
 
-def _weights(model, i):
-    L = model.layers[i]
-    return {"ln1": to_np(L.ln1), "w_qkv": to_np(L.w_qkv), "w_o": to_np(L.w_o), "ln2": to_np(L.ln2),
-            "gu_q": L.gu_q.cpu().numpy(), "gu_s": L.gu_s.cpu().numpy(),
-            "dn_q": L.dn_q.cpu().numpy(), "dn_s": L.dn_s.cpu().numpy()}
-
-
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,S", [(1, 96), (2, 64)])
 def test_layers_stage_by_stage(dev, B, S):
-    """Each stage from the GPU's own input to that stage."""
+    """Each stage from the GPU's own input to that stage (tests/stage_check.py)."""
     from shadowinfer_amd.execution import mask_tokens
+    from stage_check import check_layer_stages, weights
     m = _model(dev)
     c = m.config
     H, D, Hd = c.num_attention_heads, c.head_dim, c.hidden_size
@@ -333,47 +501,14 @@ def test_layers_stage_by_stage(dev, B, S):
     cos, sin = (to_np(t) for t in m.rope_tables(S))
     dt = O.BF16
     for i in range(c.num_hidden_layers):
-        t = {k: v for k, v in traces[i].items()}
-        W = _weights(m, i)
-        g = {k: (to_np(v) if isinstance(v, torch.Tensor) else v) for k, v in t.items()}
-        d = ulp_diff(g["xn"], R.rmsnorm(g["x"], dt, W["ln1"], c.rms_norm_eps))
-        assert d.max() <= 1 and (d > 0).mean() <= 1e-2
-        # bf16 library GEMM (fp32 accumulation, one rounding): relL2 <= 2e-3
-        assert rel_l2(f32(g["qkv"], dt), f32(R.linear(g["xn"], dt, W["w_qkv"]), dt)) <= 2e-3
-        rq, rk, rv = R.rope_split(g["qkv"], dt, cos, sin, B, S, H, D)
-        for got, want in ((g["q"], rq), (g["k"], rk)):
-            assert ulp_diff(got, want).max() <= 1
-        np.testing.assert_array_equal(g["v"], rv)
-        # the packed KV: bit-exact to the oracle pack of the GPU's own K/V
-        ref_cache = O.kv_pack(g["k"], g["v"], dt, codes[i], 16)
-        assert_cache_equal(t["cache"], ref_cache)
-        assert kv[i] is t["cache"]
-        kf, vf = O.kv_unpack(ref_cache)
-        att = O.attention(f32(g["q"], dt), kf, vf).transpose(0, 2, 1, 3)
-        # fused dequant + attention (fp16 P/V tiles) against double precision: relL2 <= 2e-3
-        assert rel_l2(f32(g["attn"], dt).reshape(B, S, H, D), att) <= 2e-3
-        x1 = f32(g["x"], dt).astype(np.float64) + \
-            f32(g["attn"], dt).reshape(B * S, Hd).astype(np.float64) @ f32(W["w_o"], dt).T.astype(np.float64)
-        assert rel_l2(f32(g["x1"], dt), x1) <= 2e-3
-        d = ulp_diff(g["y2"], R.rmsnorm(g["x1"], dt, W["ln2"], c.rms_norm_eps))
-        assert d.max() <= 1
-        qx, sx = O.int8_act_quant(g["y2"], dt)
-        np.testing.assert_array_equal(g["qx"], qx)
-        np.testing.assert_array_equal(g["sx"], sx)
-        gu = O.int8_epilogue(O.gemm_i8(g["qx"], W["gu_q"].T), g["sx"], W["gu_s"], None, dt)
-        np.testing.assert_array_equal(g["gu"], gu)
-        assert ulp_diff(g["h"], R.swiglu(g["gu"], dt)).max() <= 2
-        qh, sh = O.int8_act_quant(g["h"], dt)
-        np.testing.assert_array_equal(g["qh"], qh)
-        np.testing.assert_array_equal(g["sh"], sh)
-        ffn = O.int8_epilogue(O.gemm_i8(g["qh"], W["dn_q"].T), g["sh"], W["dn_s"], None, dt)
-        np.testing.assert_array_equal(g["ffn"], ffn)
-        out = O.from_f32(f32(g["x1"], dt) + f32(g["ffn"], dt), dt)
-        np.testing.assert_array_equal(g["out"], out)
+        assert kv[i] is traces[i]["cache"]
+        check_layer_stages(traces[i], weights(m, i), codes[i], B, S, H, D, c.rms_norm_eps, cos, sin)
     fin = traces["final"]
-    hn = R.rmsnorm(to_np(fin["hidden"]).reshape(B * S, Hd), dt, to_np(m.norm), c.rms_norm_eps)
-    assert ulp_diff(to_np(fin["hn"]).reshape(B * S, Hd), hn).max() <= 1
-    lg = R.linear(to_np(fin["hn"]).reshape(B * S, Hd), dt, to_np(m.lm_head))
+    hn, amb = R.rmsnorm(to_np(fin["hidden"]).reshape(B * S, Hd), dt, to_np(m.norm),
+                        c.rms_norm_eps, return_ambiguous=True)
+    got = to_np(fin["hn"]).reshape(B * S, Hd)
+    assert not ((got != hn).any(-1) & ~amb).any()
+    lg = R.linear(got, dt, to_np(m.lm_head))
     assert rel_l2(f32(to_np(logits), dt).reshape(B * S, -1), f32(lg, dt)) <= 2e-3
 
 
@@ -384,6 +519,7 @@ def test_step_end_to_end(dev):
     bound is relL2 <= 2e-2 on the logits (the int8 activations of the two
     chains may differ by one step where a bf16 value moved by one ulp)."""
     from shadowinfer_amd.execution import mask_tokens
+    from stage_check import weights
     m = _model(dev)
     c = m.config
     B, S = 1, 64
@@ -395,7 +531,7 @@ def test_step_end_to_end(dev):
     cos, sin = (to_np(t) for t in m.rope_tables(S))
     x = to_np(m.embed)[tokens.cpu().numpy().reshape(-1)]
     for i in range(c.num_hidden_layers):
-        x = R.layer(x, dt, _weights(m, i), codes[i], B, S, H, D, c.rms_norm_eps, cos, sin)["out"]
+        x = R.layer(x, dt, weights(m, i), codes[i], B, S, H, D, c.rms_norm_eps, cos, sin)["out"]
     lg = R.linear(R.rmsnorm(x, dt, to_np(m.norm), c.rms_norm_eps), dt, to_np(m.lm_head))
     assert rel_l2(f32(to_np(logits), dt).reshape(B * S, -1), f32(lg, dt)) <= 2e-2
 
@@ -413,20 +549,20 @@ def test_step_reuse_schedule_and_drift(dev):
                           reusable_layers={1})
     _, kv0 = m.forward_step(tokens, plans, 0, state, cfg)
     assert state.stats()["computed_layers"] == [0, 1, 2]
-    entry = state.entries[1]
+    rec = state.records[1]
     traces = {}
     tokens2 = tokens.clone()
     tokens2[0, :3] = 7
     _, kv1 = m.forward_step(tokens2, plans, 1, state, cfg, traces=traces)
     st = state.stats()
     assert st["reused_layers"] == [1] and st["computed_layers"] == [0, 2]
-    assert st["reused_ratio"] == pytest.approx(1 / 3)
+    assert st["reused_ratio"] == pytest.approx(1 / 3) and st["attention_reused"]
     assert kv1[1] is kv0[1] and kv1[0] is not kv0[0]
-    # reused layer: hidden_out + (hidden - hidden_in), bf16 elementwise ops
+    # reused layer: hidden_out + (hidden - hidden_in), the two bf16 torch ops
     h_in = traces[0]["out"].view(B, S, -1)
-    want = entry.hidden_out + (h_in - entry.hidden_in)
+    want = rec.hidden_out + (h_in - rec.hidden_in)
     assert torch.equal(traces[2]["x"].view(B, S, -1), want)
-    # drift gate (reference step_reuse.py:82-95): the same input drifts 0 -> reuse
+    # drift gate (reference step_reuse.py:71-95): the same input drifts 0 -> reuse
     state = StepReuseState()
     cfg = StepReuseConfig(enabled=True, threshold=0.05, warmup_steps=1)
     m.forward_step(tokens, plans, 0, state, cfg)
@@ -434,13 +570,44 @@ def test_step_reuse_schedule_and_drift(dev):
     assert state.stats()["reused_layers"] == []
     m.forward_step(tokens, plans, 1, state, cfg)
     assert state.stats()["reused_layers"] == [0, 1, 2]
-    assert all(d == 0.0 for d in state.last_drifts.values())
+    assert all(d == 0.0 for d in state.stats()["drifts"].values())
     other, _ = mask_tokens(B, S, 0.5, c, dev, seed=99)
     m.forward_step(other, plans, 2, state, cfg)
     assert state.stats()["computed_layers"] == [0, 1, 2]
-    assert all(d > 0.05 for d in state.last_drifts.values())
+    drifts = state.stats()["drifts"]
+    assert all(d > 0.05 for d in drifts.values())
     with pytest.raises(ValueError):
         StepReuseConfig(threshold=-1.0)
+    with pytest.raises(ValueError):
+        StepReuseConfig(warmup_steps=-1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n", [1, 7, 4096, 1 << 20, (1 << 20) + 13])
+def test_reuse_kernels_match_the_torch_ops(dev, dtype, n):
+    """The fused reuse output equals hidden_out + (hidden - hidden_in) in torch
+    bit for bit; the drift equals the reference's
+    float((hidden - hidden_in).norm() / hidden_in.norm()) in the dtype (up to
+    the fp32 summation order of the two norms: one unit in the last place of
+    the dtype, for fp32 a relative 1e-5); an all-zero hidden_in gives None."""
+    from shadowinfer_amd.execution import StepReuseState
+    from shadowinfer_amd.execution.step_reuse import LayerRecord
+    g = torch.Generator().manual_seed(n)
+    hin = torch.randn(n, generator=g).to(dtype).to(dev)
+    h = (hin.float() + 0.05 * torch.randn(n, generator=g).to(dev)).to(dtype)
+    hout = torch.randn(n, generator=g).to(dtype).to(dev)
+    st = StepReuseState()
+    rec = LayerRecord(hin, hout)
+    got = st.reuse(0, rec, h)
+    assert torch.equal(got, hout + (h - hin))
+    d = st.relative_drift(rec, h)
+    want = float((h - hin).norm() / hin.norm())
+    if dtype == torch.float32:
+        assert d == pytest.approx(want, rel=1e-5)
+    else:
+        assert abs(d - want) <= abs(float(torch.tensor(want, dtype=dtype).float()) * 2 ** -7)
+    assert st.relative_drift(LayerRecord(torch.zeros_like(hin), hout), h) is None
 
 
 @pytest.mark.gpu
@@ -458,13 +625,25 @@ def test_denoise_loop_progress(dev):
     for step in range(6):
         prev_masked = masked.clone()
         prev_tokens = tokens.clone()
-        d, kv = m.denoise_step(tokens, masked, plans, step, 0.9, state, cfg)
+        d, kv, _ = m.denoise_step(tokens, masked, plans, step, 0.9, state, cfg)
         assert bool((d.unmask <= prev_masked).all())
         assert bool(((prev_masked.sum(1) - masked.sum(1)) >= 1).all())
         assert torch.equal(tokens[d.unmask], d.tokens[d.unmask])
         assert torch.equal(tokens[~d.unmask], prev_tokens[~d.unmask])
         assert len(kv) == c.num_hidden_layers
     assert int(masked.sum()) <= int(before.sum()) - 12
+    # generate: rounds, then the forced completion by the last logits' argmax
+    tokens, masked = mask_tokens(B, S, 0.5, c, dev, seed=4)
+    start_tokens, start_masked = tokens.clone(), masked.clone()
+    seen = {}
+    res = m.generate(tokens, masked, plans, 4, 0.9, StepReuseState(), cfg,
+                     on_step=lambda st, d, kv, lg: seen.update(logits=lg, masked=masked.clone()))
+    assert not bool(masked.any()) and bool(res["finite"])
+    assert torch.equal(tokens[~start_masked], start_tokens[~start_masked])
+    left = seen["masked"]
+    assert torch.equal(res["forced"], left.sum(1))
+    assert torch.equal(tokens[left], seen["logits"].argmax(-1)[left])
+    assert torch.equal(res["unmasked_per_step"].sum(0) + res["forced"], start_masked.sum(1))
 
 
 def test_shape_validation_without_gpu():

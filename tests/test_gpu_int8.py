@@ -272,6 +272,44 @@ def test_quantizer_int8_int4_bit_exact(dev, dtype):
         Quantizer.quantize_int4(x.to(dev), group_size=24)
 
 
+def test_quantizer_dequant_broadcasts_like_torch(dev):
+    """dequantize_* is q.float() * scale with any broadcastable scale
+    (quantization.py:180-219): per-row, per-group, per-tensor, 0-d (also a 0-d
+    CPU scale, which torch broadcasts onto a device tensor), per-element and a
+    scale with more leading dims; bf16/fp16/fp32 scales; the empty round trip."""
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(-128, 128, (6, 5, 32), generator=g, dtype=torch.int8)
+    qd = q.to(dev)
+    cases = [torch.rand(6, 5, 1, generator=g), torch.rand(1, generator=g),
+             torch.rand((), generator=g), torch.rand(5, 32, generator=g),
+             torch.rand(6, 5, 32, generator=g), torch.rand(3, 1, 1, 1, generator=g)]
+    for sc in cases:
+        for dt in (torch.float32, torch.bfloat16, torch.float16):
+            s_ = sc.to(dt)
+            got = Quantizer.dequantize_int8(qd, s_.to(dev))
+            want = q.float() * s_
+            assert got.shape == want.shape and got.dtype == torch.float32
+            assert torch.equal(got.cpu(), want)
+            want_o = O.to_f32(to_np(q.expand(want.shape).contiguous()).astype(np.float32), O.F32) \
+                * O.to_f32(to_np(s_.expand(want.shape).contiguous()), DT[dt])
+            np.testing.assert_array_equal(got.cpu().numpy(), want_o)
+    s0 = torch.tensor(0.5)
+    assert torch.equal(Quantizer.dequantize_int8(qd, s0).cpu(), q.float() * s0)
+    q4 = torch.randint(-8, 8, (4, 3, 2, 16), generator=g, dtype=torch.int8)
+    for sc in (torch.rand(4, 3, 2, 1, generator=g), torch.rand((), generator=g)):
+        got = Quantizer.dequantize_int4(q4.to(dev), sc.to(dev))
+        want = (q4.float() * sc).reshape(4, 3, -1)
+        assert torch.equal(got.cpu(), want)
+    for fn in (Quantizer.quantize_int8, lambda t: Quantizer.quantize_int4(t, group_size=16)):
+        qe, se = fn(torch.empty(0, 16, device=dev))
+        de = Quantizer.dequantize_int8(qe, se)
+        assert de.shape == (0, 16) and de.dtype == torch.float32
+    with pytest.raises(TypeError):
+        Quantizer.dequantize_int8(qd, torch.rand(6, 5, 1, dtype=torch.float64, device=dev))
+    with pytest.raises(RuntimeError):
+        Quantizer.dequantize_int8(qd, torch.rand(7, 1, device=dev))
+
+
 def test_quantizer_known_answers(dev):
     """Scale of [1, -2, 3, -4] is 4/127 (reference test_kernels.py:72-77);
     zero rows get scale 1 and codes 0."""

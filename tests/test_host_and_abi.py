@@ -56,6 +56,35 @@ def test_abi_version_and_status():
     assert st["cpu_fallback"] is False and st["kv_pack_kernel"] == "hip"
 
 
+def test_status_carries_the_reference_registry_keys(monkeypatch):
+    """Every key of the reference's get_kernel_status (kernels/__init__.py:63-70,
+    78-87) with its type; the reference's caller reads
+    ['sparse_gemm_kernel'] (ffn_optimizer_agent.py:1170), which this library
+    does not provide, so it must not read "cuda" there; the
+    SHADOWINFER_FORCE_CPU_KERNELS switch (dispatcher.py:46-49) is reported and
+    refused with a clear error, since there is no CPU path."""
+    monkeypatch.delenv("SHADOWINFER_FORCE_CPU_KERNELS", raising=False)
+    st = get_kernel_status()
+    ref_keys = {"cuda_available", "cuda_extensions_loaded", "int8_kernel", "int4_kernel",
+                "sparse_gemm_kernel", "fused_attention_kernel", "autotune_cache_entries",
+                "force_cpu"}
+    assert ref_keys <= set(st)
+    assert isinstance(st["cuda_available"], bool) and isinstance(st["cuda_extensions_loaded"], bool)
+    assert st["cuda_available"] == torch.cuda.is_available()
+    assert st["cuda_extensions_loaded"] is True
+    assert st["int8_kernel"] == st["int4_kernel"] == st["fused_attention_kernel"] == "hip"
+    assert st["sparse_gemm_kernel"] == "unavailable"
+    assert st["autotune_cache_entries"] == 0 and st["force_cpu"] is False
+    monkeypatch.setenv("SHADOWINFER_FORCE_CPU_KERNELS", "1")
+    assert get_kernel_status()["force_cpu"] is True
+    with pytest.raises(RuntimeError, match="SHADOWINFER_FORCE_CPU_KERNELS"):
+        Quantizer.quantize_int8(torch.ones(2, 4))
+    with pytest.raises(RuntimeError, match="SHADOWINFER_FORCE_CPU_KERNELS"):
+        _native.call("si_act_quant_i8", 1, 9, 4, 4, 1, 1, None)
+    monkeypatch.setenv("SHADOWINFER_FORCE_CPU_KERNELS", "0")
+    assert get_kernel_status()["force_cpu"] is False
+
+
 def test_argument_validation_needs_no_device():
     """Invalid arguments are rejected before any HIP call, with a message."""
     lib = _native.load()
@@ -223,6 +252,13 @@ def test_quantizer_host_rules():
     assert q.dtype == torch.float16 and s is None
     q, s = Quantizer.quantize_int8(torch.empty(0))
     assert q.numel() == 0 and float(s) == 1.0
+    # the empty round trip: a 0-d scale broadcasts against the empty codes
+    d = Quantizer.dequantize_int8(q, s)
+    assert d.shape == (0,) and d.dtype == torch.float32
+    q4, s4 = Quantizer.quantize_int4(torch.empty(3, 0, 16))
+    assert Quantizer.dequantize_int4(q4, s4).shape == (3, 0)
+    with pytest.raises(TypeError):
+        Quantizer.dequantize_int8(q, torch.tensor(1.0, dtype=torch.float64))
     assert Quantizer.pack_int4(torch.empty(0, dtype=torch.int8)).numel() == 0
     assert Quantizer.unpack_int4(torch.empty(0, dtype=torch.uint8), (2, 3)).shape == (2, 3)
 

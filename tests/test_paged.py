@@ -323,3 +323,53 @@ def test_page_runs_equal_page_by_page(dev, precision, dtype, d):
     _eq(ga[0], wk)
     _eq(ga[1], wv)
     assert a.data_plane_bytes() == b.data_plane_bytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("precision", ["fp32", "fp16", "int8", "int4"])
+def test_pages_of_different_input_dtypes(dev, precision):
+    """Appends of bf16 and fp32 rows into one store: a new page keeps the
+    dtype of its rows, an open page takes rows of another dtype by widening to
+    torch.promote_types of the two (the reference's torch.cat of the page and
+    the new rows promotes the same way), and gather decodes every page in its
+    own dtype: the result equals the oracle decode of each segment in its
+    input dtype."""
+    kb, vb = _kv(40, s=16, dtype=torch.bfloat16)
+    kf, vf = _kv(41, s=16)
+    st = _store(dev)                                                     # pages of 8
+    st.append(kb[:, :, :8].to(dev), vb[:, :, :8].to(dev), precision)   # sealed bf16 page
+    st.append(kf[:, :, :5].to(dev), vf[:, :, :5].to(dev), precision)   # open fp32 page
+    st.append(kb[:, :, 8:10].to(dev), vb[:, :, 8:10].to(dev), precision)  # bf16 rows, fp32 page
+    assert st.page_count == 2 and [p.dtype for p in st.pages] == [torch.bfloat16, torch.float32]
+    gk, gv = st.gather()
+    for got, want in ((gk[:, :, :8], _golden(kb[:, :, :8], vb[:, :, :8], precision)),
+                      (gk[:, :, 8:13], _golden(kf[:, :, :5], vf[:, :, :5], precision)),
+                      (gk[:, :, 13:15], _golden(kb[:, :, 8:10], vb[:, :, 8:10], precision))):
+        _eq(got, want[0])
+    _eq(gv[:, :, 8:13], _golden(kf[:, :, :5], vf[:, :, :5], precision)[1])
+    # an open bf16 page that receives fp32 rows widens to fp32 (one page)
+    st2 = _store(dev)
+    st2.append(kb[:, :, :3].to(dev), vb[:, :, :3].to(dev), precision)
+    st2.append(kf[:, :, :4].to(dev), vf[:, :, :4].to(dev), precision)
+    assert st2.page_count == 1 and st2.pages[0].dtype == torch.float32
+    g2k, g2v = st2.gather()
+    _eq(g2k[:, :, :3], _golden(kb[:, :, :3], vb[:, :, :3], precision)[0])
+    _eq(g2v[:, :, 3:], _golden(kf[:, :, :4], vf[:, :, :4], precision)[1])
+
+
+@pytest.mark.gpu
+def test_rewrite_with_another_input_dtype(dev):
+    """fp32 rows rewritten into a bf16 int8 page: quantized in fp32, then the
+    scales stored in the page's bf16 (the reference's copy_ into the page)."""
+    kb, vb = _kv(42, s=8, dtype=torch.bfloat16)
+    kf, vf = _kv(43, s=8)
+    st = _store(dev)
+    st.append(kb.to(dev), vb.to(dev), "int8")
+    st.rewrite_tokens(2, kf[:, :, 2:5].to(dev), vf[:, :, 2:5].to(dev), "int8")
+    gk, _ = st.gather()
+    rows = to_np(kf[:, :, 2:5])                                          # [B, H, 3, D] fp32
+    q, s = O.quant_rows_i8(rows, O.F32)
+    s16 = O.from_f32(s, O.BF16)
+    want = O.dequant_rows(q, s16, O.BF16, D)
+    _eq(gk[:, :, 2:5], want)
+    _eq(gk[:, :, :2], _golden(kb[:, :, :2], vb[:, :, :2], "int8")[0])
