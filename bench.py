@@ -526,20 +526,23 @@ def bench_step(torch, dev, steps=8, warmup=2, gen_steps=64):
         lambda: model.denoise_step(tokens, masked, plans, next(it), 0.9, state, reuse_cfg), steps)
     res["reused_ratio"] = state.stats()["reused_ratio"]
 
-    # a whole generation: step 0 computes every layer, then 63 reuse steps
+    # a whole generation: step 0 computes every layer, then 63 reuse steps,
+    # then the forced completion of what is still masked
     tokens, masked, state = fresh()
     n_masked = int(masked.sum())
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for step in range(gen_steps):
-        model.denoise_step(tokens, masked, plans, step, 0.9, state, reuse_cfg)
+    gen = model.generate(tokens, masked, plans, gen_steps, 0.9, state, reuse_cfg)
     end.record(stream)
     end.synchronize()
     res["generation_ms"] = start.elapsed_time(end)
     res["generation_steps"] = gen_steps
-    res["unmasked_in_generation"] = n_masked - int(masked.sum())
+    res["unmasked_in_rounds"] = int(gen["unmasked_per_step"].sum())
+    res["forced_completions"] = int(gen["forced"].sum())
+    res["masked_at_start"] = n_masked
+    res["all_resolved"] = not bool(masked.any())
     res["positions_per_s"] = Sd / (res["step_ms"] * 1e-3)
     return res
 

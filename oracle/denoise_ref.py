@@ -131,9 +131,11 @@ def swiglu(gu: np.ndarray, dt: int, return_ambiguous: bool = False):
         return h
     with np.errstate(invalid="ignore"):
         ulp = np.abs(np.spacing(s32.astype(np.float32)).astype(np.float64))
-        lo = _round(s32 - 4 * ulp, dt)
-        hi = _round(s32 + 4 * ulp, dt)
-    return h, lo != hi
+        lo = _f64(_round(s32 - 4 * ulp, dt), dt)
+        hi = _f64(_round(s32 + 4 * ulp, dt), dt)
+    # an exact zero (g = 0, or exp overflowing for g << 0) has no neighbour to
+    # round to; -0 and +0 compare equal above
+    return h, (lo != hi) & (s32 != 0)
 
 
 def argmax_conf(logits: np.ndarray, dt: int, sum_rel_err: float = SUM_REL_ERR,

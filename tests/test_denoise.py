@@ -353,11 +353,14 @@ def test_swiglu_kernel(dev, dtype, M, F):
     h, q, s = row_ops.swiglu_quant(gu.to(dev), want_h=True)
     dt = DT[dtype]
     gd = gu.to(dev)
-    torch_h = F.silu(gd[:, :F]) * gd[:, F:]
+    torch_h = torch.nn.functional.silu(gd[:, :F]) * gd[:, F:]
     assert torch.equal(h, torch_h)
     want, amb = R.swiglu(to_np(gu), dt, return_ambiguous=True)
-    assert amb.mean() < 0.01
-    np.testing.assert_array_equal(to_np(h)[~amb], want[~amb])
+    if dtype == torch.float32:      # no rounding to absorb the device expf's ulp
+        np.testing.assert_allclose(to_np(h), want, rtol=4 * 2.0 ** -23, atol=1e-37)
+    else:
+        assert amb.mean() < 0.01
+        np.testing.assert_array_equal(to_np(h)[~amb], want[~amb])
     qr, sr = O.int8_act_quant(to_np(h), dt)
     np.testing.assert_array_equal(to_np(q), qr)
     np.testing.assert_array_equal(to_np(s), sr)
@@ -440,7 +443,10 @@ def test_schedule_round_matches_reference_rule(dev):
                 ru, rt, rc, rf = _reference_schedule(lg, mk, thr)
                 assert torch.equal(d.unmask, ru) and torch.equal(d.progress_fallback, rf)
                 assert torch.equal(d.tokens[d.unmask], rt[d.unmask])
-                assert torch.equal(d.confidences, rc)
+                if dtype == torch.float32:   # fp32 sums in another order: last bits
+                    torch.testing.assert_close(d.confidences, rc, rtol=4 * R.SUM_REL_ERR, atol=0)
+                else:
+                    assert torch.equal(d.confidences, rc)
                 _, conf = R.argmax_conf(to_np(lg), DT[dtype])
                 ou, of = R.schedule(conf, mk.cpu().numpy(), thr, DT[dtype])
                 np.testing.assert_array_equal(d.unmask.cpu().numpy(), ou)

@@ -134,7 +134,10 @@ def test_config3_reuse_50_percent_7b_layer(dev, same_plan):
     t, h = np.nonzero(mask)
     rstats = O.kv_apply_reuse_mask(ref, ref_prev, {(int(a), int(b)): True for a, b in zip(t, h)})
     assert stats == rstats
-    assert stats["applied"] > 0.2 * S * H
+    # half the entries are masked; with two independent 25/50/25 plans an entry
+    # keeps its precision with probability 0.375
+    share = 0.5 if same_plan else 0.5 * 0.375
+    assert abs(stats["applied"] / (S * H) - share) < 0.01
     if not same_plan:
-        assert stats["skipped_precision"] > 0
+        assert abs(stats["skipped_precision"] / (S * H) - 0.5 * 0.625) < 0.01
     assert_cache_equal(cur, ref)
