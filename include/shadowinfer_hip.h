@@ -307,6 +307,23 @@ int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64
                            void* out, void* workspace, size_t workspace_bytes,
                            si_stream_t stream);
 
+/* Size of the device scratch array of si_int8_linear_forward_noalloc (one
+ * per device, held until the process ends). */
+#define SI_INT8_LINEAR_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* No counterpart in the reference: si_int8_linear_forward for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results, no
+ * workspace argument: the workspace is a library-owned device array of
+ * SI_INT8_LINEAR_SCRATCH_BYTES per device, so shapes whose
+ * si_int8_linear_workspace_bytes(M, K, N) exceeds it are rejected
+ * (SI_ERR_INVALID). Allocates nothing. The first call on a device looks the
+ * array up (call it once before capturing). Calls that overlap on one device
+ * (other streams, other threads) share the array and race: order them. */
+int si_int8_linear_forward_noalloc(const void* x, int dtype, int64_t M, int64_t K, int64_t N,
+                                   const int8_t* qweight, const float* sw, const float* bias,
+                                   void* out, si_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Paged KV store                                                          */
 /* ---------------------------------------------------------------------- */

@@ -28,6 +28,8 @@
 // the result does not depend on the order).
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "si_common.h"
 
 namespace si {
@@ -1183,4 +1185,67 @@ extern "C" int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64
   if (int rc = si_act_quant_i8(x, dtype, M, K, q, sx, stream)) return rc;
   return si_gemm_i8_dequant(q, sx, qweight, sw, bias, M, N, K, out, dtype, gws,
                             workspace_bytes - qbytes - sbytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// si_int8_linear_forward_noalloc: si_int8_linear_forward with its workspace
+// (quantized activations, their scales, split-K partials) in `scratch`, a
+// file-scope device array, instead of caller memory, for callers that cannot
+// allocate. Every device holds its own copy until the process ends. The host
+// never passes the array's name to a kernel: it looks the array's device
+// address up once per device (hipGetSymbolAddress, with that device current)
+// and uses that address. No entry here allocates device memory.
+// ---------------------------------------------------------------------------
+namespace si {
+namespace {
+
+constexpr size_t kScratchBytes = SI_INT8_LINEAR_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, or nullptr (error set).
+void* scratch_here(const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current device (%s, device %d)", who, hipGetErrorString(e), dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", who,
+                dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+}  // namespace si
+
+extern "C" int si_int8_linear_forward_noalloc(const void* x, int dtype, int64_t M, int64_t K,
+                                              int64_t N, const int8_t* qweight, const float* sw,
+                                              const float* bias, void* out, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_int8_linear_forward_noalloc: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(M >= 0 && K > 0 && N > 0, "si_int8_linear_forward_noalloc: bad shape");
+  if (M == 0) return SI_OK;
+  SI_CHECK_ARG(x && qweight && sw && out, "si_int8_linear_forward_noalloc: NULL argument");
+  const size_t need = si_int8_linear_workspace_bytes(M, K, N);
+  SI_CHECK_ARG(need <= kScratchBytes,
+               "si_int8_linear_forward_noalloc: this shape needs %zu bytes of workspace, more "
+               "than the %zu-byte scratch; use si_int8_linear_forward with a workspace",
+               need, kScratchBytes);
+  void* ws = scratch_here("si_int8_linear_forward_noalloc");
+  if (ws == nullptr) return SI_ERR_HIP;
+  return si_int8_linear_forward(x, dtype, M, K, N, qweight, sw, bias, out, ws, kScratchBytes,
+                                stream);
 }

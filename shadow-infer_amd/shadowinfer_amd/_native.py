@@ -99,6 +99,8 @@ _SIGNATURES = {
     "si_int8_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "si_int8_linear_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                       _sz, _vp]),
+    "si_int8_linear_forward_noalloc": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                                              _vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
