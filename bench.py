@@ -5,18 +5,22 @@ cache - 32 layers x B=1 x S=8192 x H=32 x D=128, bf16 K/V ~ N(0,1) with 1%
 outlier channels x8, precision codes 25% fp16 / 50% int8 / 25% int4 (group
 16) with a 4-token fp16 sink. One step = for every layer, pack (dense K/V ->
 precision buckets) then unpack (buckets -> fp32 K/V); inputs, plans and
-buckets are resident in HBM before the timed region. Throughput counts the
-algorithmic bytes: pack reads K+V and the code matrix and writes the packed
-bytes; unpack reads the packed bytes and the codes and writes fp32 K+V
-(slot metadata excluded).
+buckets are resident in HBM before the timed region. Before every launch the
+L2s and the Infinity Cache are flushed (a 512 MiB read, which leaves no dirty
+line behind), and each launch is timed alone with a HIP event pair on its
+stream; the step time is the sum.
+The same step back to back without flushes is reported as ``kv.warm_*``.
+Throughput counts the algorithmic bytes: pack reads K+V and the code matrix
+and writes the packed bytes; unpack reads the packed bytes and the codes and
+writes fp32 K+V (slot metadata excluded).
 
 Also reported on the same JSON line: per-kernel times with the roofline of the
 dominant kernel, the INT8 FFN GEMM (4096 x 11008, M in {16, 64, 256, 1024}) in
 TOPS against the int8 MFMA peak, the fused packed-KV attention, the
 rate-distortion admission of one layer (sensitivity proxy + budget solver),
 the paged KV store of one layer (prefill append, append, gather),
-and the CPU baseline (the oracle on the host, a bounded sample of the same
-workload).
+and the CPU baseline: the reference's own torch op chain on the host (a
+bounded sample of the same workload, all cores of this job and 1 thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--part all|kv|gemm|attention|admit|paged|step|calib]
@@ -41,6 +45,7 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16/bf16 MFMA, TFLOP/s
 LAYERS, B, S, H, D = 32, 1, 8192, 32, 128
 GROUP = 16
 CALIB_BYTES = 512 << 20
+FLUSH_BYTES = 512 << 20      # > 256 MB Infinity Cache + 8 x 4 MB L2
 
 
 def log(msg: str) -> None:
@@ -156,18 +161,66 @@ def bench_kv(torch, dev, steps, warmup):
     ms_unpack = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / len(evs)
     avg_pack_b = sum(pack_bytes) / LAYERS
     avg_unpack_b = sum(unpack_bytes) / LAYERS
+
+    # Flushed protocol (the headline): before every pack and every unpack
+    # launch a FLUSH_BYTES buffer is read in full (a sum), which replaces the
+    # contents of the 256 MB Infinity Cache and of every L2 with clean lines,
+    # so each launch reads its inputs from HBM and no earlier write is still
+    # waiting to be written back (a flush by overwriting would leave that
+    # write-back to the timed launch); each launch is timed alone with an
+    # event pair on its stream. A step is the 32 packs and 32 unpacks; its
+    # time is the sum of their launch times.
+    flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+
+    def flush(i):
+        flush_buf.sum(dtype=torch.int64)
+
+    for i, L in enumerate(layers[:2]):
+        flush(i)
+        pack(L)
+        flush(i + 1)
+        unpack(L)
+    fev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(LAYERS * steps)]
+    torch.cuda.synchronize()
+    for r in range(steps):
+        for i, L in enumerate(layers):
+            e = fev[r * LAYERS + i]
+            flush(2 * i)
+            e[0].record(stream)
+            pack(L)
+            e[1].record(stream)
+            flush(2 * i + 1)
+            e[2].record(stream)
+            unpack(L)
+            e[3].record(stream)
+    torch.cuda.synchronize()
+    f_pack = [e[0].elapsed_time(e[1]) for e in fev]
+    f_unpack = [e[2].elapsed_time(e[3]) for e in fev]
+    f_step_ms = (sum(f_pack) + sum(f_unpack)) / steps
+    fp = sum(f_pack) / len(f_pack)
+    fu = sum(f_unpack) / len(f_unpack)
+    del flush_buf
     res = {
-        "ms_per_step": ms_step,
-        "wall_ms_per_step": wall,
+        "protocol": f"caches flushed (a {FLUSH_BYTES >> 20} MiB read) before every launch; "
+                    "each launch timed alone with an event pair",
+        "ms_per_step": f_step_ms,
         "step_bytes": step_bytes,
-        "gbs": step_bytes / (ms_step * 1e-3) / 1e9,
-        "pack_us": ms_pack * 1e3,
-        "unpack_us": ms_unpack * 1e3,
-        "pack_gbs": avg_pack_b / (ms_pack * 1e-3) / 1e9,
-        "unpack_gbs": avg_unpack_b / (ms_unpack * 1e-3) / 1e9,
+        "gbs": step_bytes / (f_step_ms * 1e-3) / 1e9,
+        "pack_us": fp * 1e3,
+        "unpack_us": fu * 1e3,
+        "pack_gbs": avg_pack_b / (fp * 1e-3) / 1e9,
+        "unpack_gbs": avg_unpack_b / (fu * 1e-3) / 1e9,
         "pack_bytes_per_launch": avg_pack_b,
         "unpack_bytes_per_launch": avg_unpack_b,
         "packed_bytes_per_layer": sum(L["packed"] for L in layers) / LAYERS,
+        # back to back, no flush: each unpack follows its own layer's pack
+        "warm_ms_per_step": ms_step,
+        "warm_wall_ms_per_step": wall,
+        "warm_gbs": step_bytes / (ms_step * 1e-3) / 1e9,
+        "warm_pack_us": ms_pack * 1e3,
+        "warm_unpack_us": ms_unpack * 1e3,
+        "warm_pack_gbs": avg_pack_b / (ms_pack * 1e-3) / 1e9,
+        "warm_unpack_gbs": avg_unpack_b / (ms_unpack * 1e-3) / 1e9,
     }
 
     # The reference-API path (plan given, buckets allocated per call, unpack
@@ -547,60 +600,143 @@ def bench_step(torch, dev, steps=8, warmup=2, gen_steps=64):
     return res
 
 
-def cpu_baseline(layers: int = 16):
-    """The oracle (C + numpy, one thread) on ``layers`` of the 32 layers (each
-    layer's own precision codes, one seeded K/V): pack + unpack, algorithmic
-    bytes / wall time of the oracle calls (about 10 s)."""
+def host_cpu():
+    """CPU model name and CPU counts of the host this runs on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        import psutil
+        physical = psutil.cpu_count(logical=False)
+    except Exception:
+        physical = None
+    return {"cpu_model": model, "host_logical_cpus": os.cpu_count(),
+            "host_physical_cores": physical, "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def all_threads() -> int:
+    """Threads for the all-cores leg: this job's CPU share (OMP_NUM_THREADS
+    when set, as on the GPU box), else the CPUs in the affinity mask, at most
+    the physical cores."""
+    info = host_cpu()
+    n = info["affinity_cpus"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        n = min(n, int(os.environ["OMP_NUM_THREADS"]))
+    if info["host_physical_cores"]:
+        n = min(n, info["host_physical_cores"])
+    return max(1, n)
+
+
+def _stats(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2], xs[0], xs[-1]
+
+
+def cpu_baseline(layers_all: int = 5, layers_one: int = 3):
+    """The reference's CPU path for the headline workload: the torch op chain
+    of PackedKVCache._do_pack_with_plan + unpack (oracle/torch_ref.py) on one
+    7B layer at a time (each layer its own K/V and codes, the plan built
+    beforehand as the reference's pack receives it), timed with perf_counter
+    after a warm-up layer, once with torch.set_num_threads(all cores of this
+    job) and once with 1 thread. GB/s over the same algorithmic bytes as the
+    GPU line."""
     import numpy as np
     import torch
-    sys.path.insert(0, ROOT)
-    from oracle import oracle as O
 
-    O.build()
-    total_bytes, total_s = 0, 0.0
+    sys.path.insert(0, ROOT)
+    from oracle import torch_ref as TR
+
     gen = torch.Generator().manual_seed(99)
-    k = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
-    v = torch.randn(B, H, S, D, generator=gen).to(torch.bfloat16)
-    kn = k.view(torch.int16).numpy().view(np.uint16)
-    vn = v.view(torch.int16).numpy().view(np.uint16)
-    for layer in range(layers):
-        codes = make_codes(1000 + layer)
-        t0 = time.perf_counter()
-        cache = O.kv_pack(kn, vn, O.BF16, codes, GROUP)
-        O.kv_unpack(cache)
-        total_s += time.perf_counter() - t0
-        packed = cache.memory_bytes()
-        total_bytes += (2 * B * H * S * D * 2 + S * H + packed) + (packed + S * H + 2 * B * H * S * D * 4)
-    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{layers} of the 32 layers (pack+unpack), oracle in C + numpy, 1 thread",
-            "seconds": total_s}
+    prev_threads = torch.get_num_threads()
+
+    def layer_inputs(i):
+        k = torch.randn(B, H, S, D, generator=gen)
+        v = torch.randn(B, H, S, D, generator=gen)
+        ch = torch.randperm(D, generator=gen)[: max(1, round(0.01 * D))]
+        k[..., ch] *= 8
+        v[..., ch] *= 8
+        groups, flat = TR.plan_from_codes(torch.from_numpy(make_codes(1000 + i)))
+        return k.to(torch.bfloat16), v.to(torch.bfloat16), groups, flat
+
+    def run(threads, n):
+        torch.set_num_threads(threads)
+        rates, times = [], []
+        for i in range(n + 1):
+            k, v, groups, flat = layer_inputs(i)
+            t0 = time.perf_counter()
+            packed = TR.pack_with_plan(k, v, groups, flat, GROUP)
+            TR.unpack(packed, B, H, S, D)
+            dt = time.perf_counter() - t0
+            pbytes = sum(t.numel() * t.element_size() for d in packed.values()
+                         for key in ("k", "v", "scale_k", "scale_v")
+                         for t in [d.get(key)] if t is not None)
+            nbytes = (2 * B * H * S * D * 2 + S * H + pbytes) + (pbytes + S * H + 2 * B * H * S * D * 4)
+            if i:                       # layer 0 warms up
+                rates.append(nbytes / dt / 1e9)
+                times.append(dt * 1e3)
+        med, lo, hi = _stats(rates)
+        return {"threads": threads, "layers": n, "median_gbs": med, "min_gbs": lo, "max_gbs": hi,
+                "median_layer_ms": _stats(times)[0]}
+
+    n_all = all_threads()
+    t0 = time.perf_counter()
+    res_all = run(n_all, layers_all)
+    res_one = run(1, layers_one)
+    torch.set_num_threads(prev_threads)
+    return {"value": res_all["median_gbs"], "unit": "GB/s", "cores": n_all, "kind": "port",
+            "sample": f"pack+unpack of one 7B layer at a time (1 x 32 x 8192 x 128 bf16, the "
+                      f"headline's codes), the reference's torch op chain on the host: "
+                      f"{layers_all} layers with {n_all} threads, {layers_one} with 1 thread, "
+                      "median over layers after one warm-up layer",
+            "threads_all": res_all, "threads_1": res_one, **host_cpu(),
+            "seconds": time.perf_counter() - t0}
 
 
-def cpu_gemm_baseline(ms=(16, 64)):
-    """The oracle's INT8Linear forward (C, one thread: activation quant, int8 x
-    int8 -> int32 GEMM, epilogue) on the 4096 x 11008 FFN shape for the given
-    M, on the host: microseconds and TOPS per M."""
-    import numpy as np
+def cpu_gemm_baseline(ms=(16, 64, 256, 1024), reps_all=5, reps_one=3):
+    """INT8Linear.forward's torch op chain with CPU torch._int_mm
+    (oracle/torch_ref.py) on M x 4096 x 11008, bf16 input, weights N(0, 0.02)
+    quantized per channel: median and range of ``reps`` calls after two
+    warm-ups, with all cores of this job and with 1 thread."""
+    import torch
+
     sys.path.insert(0, ROOT)
-    from oracle import oracle as O
+    from oracle import torch_ref as TR
 
-    O.build()
     K, N = 4096, 11008
-    rng = np.random.default_rng(5)
-    w = rng.standard_normal((K, N), dtype=np.float32) * 0.02
-    sw = (np.abs(w).max(axis=0) / 127).astype(np.float32)
-    qw = np.clip(np.rint(w / sw), -127, 127).astype(np.int8)  # [K, N], the reference's layout
-    out = {}
-    for M in ms:
-        x = rng.standard_normal((M, K), dtype=np.float32)
-        xb = (x.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated draw)
-        t0 = time.perf_counter()
-        O.int8_linear_forward(xb, O.BF16, qw, sw)
-        dt = time.perf_counter() - t0
-        out[str(M)] = {"us": dt * 1e6, "tops": 2.0 * M * K * N / dt / 1e12}
-    return {"kind": "port", "cores": 1,
-            "sample": "oracle INT8Linear forward (C, 1 thread) on 4096 x 11008, M in "
-                      + ", ".join(str(m) for m in ms), **out}
+    gen = torch.Generator().manual_seed(5)
+    qw, sw = TR.int8_weight(torch.randn(N, K, generator=gen) * 0.02)
+    prev_threads = torch.get_num_threads()
+
+    def run(threads, reps):
+        torch.set_num_threads(threads)
+        out = {"threads": threads}
+        for M in ms:
+            x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+            for _ in range(2):
+                TR.int8_linear_forward(x, qw, sw)
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                TR.int8_linear_forward(x, qw, sw)
+                ts.append(time.perf_counter() - t0)
+            med, lo, hi = _stats(ts)
+            out[str(M)] = {"ms": med * 1e3, "min_ms": lo * 1e3, "max_ms": hi * 1e3,
+                           "tops": 2.0 * M * K * N / med / 1e12}
+        return out
+
+    n_all = all_threads()
+    res = {"kind": "port", "cores": n_all,
+           "sample": "INT8Linear forward torch op chain with CPU torch._int_mm, M x 4096 x 11008, "
+                     f"median of {reps_all} ({n_all} threads) / {reps_one} (1 thread) calls",
+           "threads_all": run(n_all, reps_all), "threads_1": run(1, reps_one), **host_cpu()}
+    torch.set_num_threads(prev_threads)
+    return res
 
 
 def measured_traffic(kernel: str):
@@ -617,6 +753,14 @@ def measured_traffic(kernel: str):
     except OSError:
         pass
     return None
+
+
+def _rounded(obj, nd=4):
+    if isinstance(obj, float):
+        return round(obj, nd)
+    if isinstance(obj, dict):
+        return {k: _rounded(v, nd) for k, v in obj.items()}
+    return obj
 
 
 def main():
@@ -664,7 +808,8 @@ def main():
         return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
-    log(f"kv {kv['gbs']:.1f} GB/s, pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us")
+    log(f"kv flushed {kv['gbs']:.1f} GB/s (pack {kv['pack_us']:.1f} us, unpack "
+        f"{kv['unpack_us']:.1f} us); warm {kv['warm_gbs']:.1f} GB/s")
     gemm = attn = adm = paged = step = None
     if args.part == "all":
         log("int8 gemm")
@@ -680,13 +825,14 @@ def main():
     cpu = None
     gemm_cpu = None
     if not args.no_cpu:
-        log("cpu baseline (oracle)")
+        log("cpu baseline (the reference's torch op chain on the host)")
         cpu = cpu_baseline()
-        log(f"cpu {cpu['value']:.3f} GB/s in {cpu['seconds']:.1f} s")
+        log(f"cpu {cpu['value']:.3f} GB/s ({cpu['cores']} threads), "
+            f"{cpu['threads_1']['median_gbs']:.3f} GB/s (1 thread) in {cpu['seconds']:.1f} s")
         if gemm is not None:
             gemm_cpu = cpu_gemm_baseline()
-            log("cpu gemm " + ", ".join(f"M={m} {gemm_cpu[m]['us'] / 1e3:.0f} ms"
-                                         for m in ("16", "64")))
+            log("cpu gemm " + ", ".join(f"M={m} {gemm_cpu['threads_all'][m]['ms']:.2f} ms"
+                                         for m in ("16", "64", "256", "1024")))
 
     dom = "unpack" if kv["unpack_us"] >= kv["pack_us"] else "pack"
     achieved = kv[f"{dom}_gbs"]
@@ -708,6 +854,7 @@ def main():
                         "bf16 K/V, codes 25% fp16 / 50% int8 / 25% int4 g16, 4-token fp16 sink",
             "layers": LAYERS, "batch": B, "seq_len": S, "heads": H, "head_dim": D,
             "int4_group": GROUP, "hbm_frac": round(kv["gbs"] / HBM_PEAK_GBS, 4),
+            "protocol": "caches flushed before every pack and unpack launch",
         },
         "roofline": {
             "kernel": f"kv_{dom}",
@@ -717,20 +864,20 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(f"kv_{dom}"),
+            "traffic_source": "profiles/kv_7b_layer_hbm_traffic.txt: rocprofv3 --pmc FETCH_SIZE "
+                              "and WRITE_SIZE per dispatch of this bench's kv part, each scaled "
+                              "by the counter's reading for a plain device copy",
             "bytes_per_launch": int(kv[f"{dom}_bytes_per_launch"]),
             "avg_launch_us": round(kv[f"{dom}_us"], 3),
         },
-        "cpu_baseline": cpu and {k: (round(v, 4) if isinstance(v, float) else v)
-                                 for k, v in cpu.items() if k != "seconds"},
+        "cpu_baseline": cpu and _rounded({k: v for k, v in cpu.items() if k != "seconds"}),
         "kv": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in kv.items()},
     }
     if gemm is not None:
         line["int8_gemm"] = {"shape": "M x 4096 x 11008", "peak_tops": INT8_PEAK_TOPS,
                              **{m: {k: round(v, 4) for k, v in r.items()} for m, r in gemm.items()}}
         if gemm_cpu is not None:
-            line["int8_gemm"]["cpu_baseline"] = {
-                k: ({kk: round(vv, 4) for kk, vv in v.items()} if isinstance(v, dict) else v)
-                for k, v in gemm_cpu.items()}
+            line["int8_gemm"]["cpu_baseline"] = _rounded(gemm_cpu)
     if attn is not None:
         line["packed_attention"] = {"shape": "B=1, H=32, D=128, S_q=S_kv", "peak_tflops": FP16_PEAK_TFLOPS,
                                     **{s: {k: round(v, 4) for k, v in r.items()} for s, r in attn.items()}}
