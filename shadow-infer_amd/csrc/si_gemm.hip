@@ -752,6 +752,146 @@ __global__ __launch_bounds__(64 * NW) void gemm_stream(const int8_t* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row-block streaming kernel (M <= 16*MF, one block per CU): a block owns RB
+// <= 16*G consecutive weight rows over the full K, so the weight is read once
+// and split evenly over the CUs (4096 x 11008: 43 rows per block, 256 blocks).
+// Stage s holds k bytes [256 ks, 256 ks + 256) of the block's weight rows (LDS
+// rows 0 .. 16G-1) and of the activation rows (LDS rows 16G .. 16G+16MF-1):
+// each copy is one global_load_lds_dwordx4 of 4 rows x 256 contiguous bytes
+// (row runs of 256 B keep the HBM bursts whole, where the 64-byte row pieces
+// of direct fragment loads do not), chunk p of row r stored at slot p ^ (r &
+// 15) so that the 16 rows of one fragment read fall on distinct banks. R
+// stages rotate with one barrier per stage; wave w multiplies k step w of each
+// stage for all G row groups, and the four waves' partial sums over disjoint
+// k are added in LDS at the end. Blocks start their k loop at different
+// stages (the int32 sums do not depend on the order), which spreads the CUs
+// of one XCD over different activation lines. The epilogue's scales are
+// loaded before the first stage, so no load waits in the tail.
+// Requires K % 256 == 0 and 1 <= RB <= 16*G.
+// ---------------------------------------------------------------------------
+template <int IPW, int I>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (I <= 0) {
+    wait_cnt<0, 15>();
+  } else {
+    if (n >= I) wait_cnt<I * IPW, 15>();
+    else wait_stages<IPW, I - 1>(n);
+  }
+}
+
+template <int MF, int G, int R, int EPI>
+__global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
+                                                 const int8_t* __restrict__ B, int M, int N, int K,
+                                                 int RB, int32_t* __restrict__ C, EpiArgs ep) {
+  constexpr int TR = 16 * (G + MF);  // LDS rows per stage
+  constexpr int STAGE = TR * 256;
+  constexpr int IPW = TR / 16;       // copies per wave per stage
+  static_assert((R - 2) * IPW <= 63, "vmcnt holds at most 63 outstanding loads");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[R * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * RB;
+  const int nrows = min(RB, N - n0);
+  const int stages = K / 256;
+  const int rot = (blockIdx.x >> 3) % stages;
+  // copy j of wave w fills LDS rows 4(4j + w) .. +3; padding rows re-read the
+  // block's last weight row (an L2 hit) instead of another block's rows
+  const int8_t* src[IPW];
+#pragma unroll
+  for (int j = 0; j < IPW; ++j) {
+    const int r = 4 * (4 * j + w) + (lane >> 4);
+    const int8_t* row = r < 16 * G ? B + (int64_t)(n0 + min(r, nrows - 1)) * K
+                                   : A + (int64_t)min(r - 16 * G, M - 1) * K;
+    src[j] = row + 16 * ((lane & 15) ^ (r & 15));
+  }
+  auto issue = [&](int s, int slot) {
+    int ks = s + rot;
+    ks = ks >= stages ? ks - stages : ks;
+    int8_t* dst = lds + slot * STAGE + 1024 * w;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j)
+      __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + 256 * ks), (lvoid_t*)(dst + 4096 * j),
+                                       16, 0, 0);
+  };
+  // this thread's outputs are e = threadIdx.x + 256 x: row e / nrows, column e % nrows
+  constexpr int EPT = MF * G;
+  const int mm = min(M, 16 * MF);
+  float esx[EPT], esw[EPT], eb[EPT];
+#pragma unroll
+  for (int x = 0; x < EPT; ++x) {
+    const int e = threadIdx.x + 256 * x;
+    const int m = e / nrows, jj = e - m * nrows;
+    esx[x] = esw[x] = eb[x] = 0.0f;
+    if (EPI == EPI_DEQUANT && m < mm) {
+      esx[x] = ep.sx[m];
+      esw[x] = ep.sw[n0 + jj];
+      if (ep.bias != nullptr) eb[x] = ep.bias[n0 + jj];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < R - 1; ++u)
+    if (u < stages) issue(u, u);
+  const int fr = lane & 15, fc = lane >> 4;
+  const int foff = 256 * fr + 16 * ((4 * w + fc) ^ fr);  // k step w of a 16-row group
+  v4i acc[G][MF];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < MF; ++i) acc[g][i] = v4i{0, 0, 0, 0};
+  int slot = 0;
+  for (int s = 0; s < stages; ++s) {
+    wait_stages<IPW, R - 2>(stages - 1 - s);  // stages s+1 .. s+R-2 may stay in flight
+    bare_barrier();                            // every wave's copies of stage s landed;
+    if (s + R - 1 < stages)                    // every wave is done with stage s-1
+      issue(s + R - 1, slot == 0 ? R - 1 : slot - 1);
+    const int8_t* base = lds + slot * STAGE + foff;
+    v4i a[MF], b[G];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) a[i] = *reinterpret_cast<const v4i*>(base + 4096 * (G + i));
+#pragma unroll
+    for (int g = 0; g < G; ++g) b[g] = *reinterpret_cast<const v4i*>(base + 4096 * g);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+        acc[g][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[g], acc[g][i], 0, 0, 0);
+    slot = slot == R - 1 ? 0 : slot + 1;
+  }
+  __syncthreads();
+  // accumulator register r of (g, i): activation row 16i + 4(lane/16) + r,
+  // weight row 16g + lane%16
+  constexpr int RP = 16 * MF + 4;
+  constexpr int PART = 16 * G * RP;
+  static_assert(4 * PART * 4 <= R * STAGE, "reduction area");
+  int32_t* red = reinterpret_cast<int32_t*>(lds);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[w * PART + (16 * g + fr) * RP + 16 * i + 4 * fc + r] = acc[g][i][r];
+  __syncthreads();
+#pragma unroll
+  for (int x = 0; x < EPT; ++x) {
+    const int e = threadIdx.x + 256 * x;
+    const int m = e / nrows, jj = e - m * nrows;
+    if (m < mm) {
+      int32_t v = 0;
+#pragma unroll
+      for (int y = 0; y < 4; ++y) v += red[y * PART + jj * RP + m];
+      if (EPI == EPI_DEQUANT) {
+        float o = (float)v * (esx[x] * esw[x]);
+        if (ep.bias != nullptr) o = o + eb[x];
+        store_any(ep.out, ep.out_dtype, (int64_t)m * N + n0 + jj, o);
+      } else {
+        epi_store<EPI>(ep, C, M, N, m, n0 + jj, v, 0);
+      }
+    }
+  }
+}
+
 // Sum split-K partials (exact integer adds) and store int32 or dequantized.
 __global__ __launch_bounds__(256) void gemm_finalize(const int32_t* __restrict__ partial,
                                                      int splits, int64_t M, int64_t N,
@@ -808,7 +948,9 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             K_STREAM_N32 = 32, K_STREAM_N16 = 33, K_STREAM_N32_W8 = 34, K_STREAM_N16_W8 = 35,
             // 64-row tiles of the small-M choice (choose_fill): less row padding and
             // more blocks than 128x128 when few rows share the weight
-            K_DMA_64x64 = 38, K_DMA_64x128 = 39 };
+            K_DMA_64x64 = 38, K_DMA_64x128 = 39,
+            // one block per CU over ceil(N / 256) weight rows (gemm_rows)
+            K_ROWS = 40 };
 
 struct Plan {
   int kind;
@@ -873,8 +1015,15 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   if (K % 16 != 0 || M == 0 || N == 0 || big) return p;
   int kind;
   int fill_splits = 0;
+  const int64_t rows_per_cu = ceil_div(N, 256);
   if (forced_kind() >= 0) {
     kind = forced_kind();
+  } else if (M <= 32 && K % 256 == 0 && rows_per_cu >= 16 && rows_per_cu <= 48) {
+    // Each CU streams its own ceil(N / 256) weight rows once: 11008 x 4096 at
+    // M = 16 / 32: 14.1 / 14.7 -> 10.2 / 11.3 us; 4096 x 11008: 14.0 / 15.0 ->
+    // 13.6 / 14.5 us. From 33 rows the activation copies outweigh the weight's
+    // and the tile kernels are as fast.
+    kind = K_ROWS;
   } else if (K % 128 == 0 && M <= 128 &&
              (M > 16 || (M > 8 && ceil_div(N, 64) >= 128 && ceil_div(N, 64) < 256))) {
     // From 9 rows, where the stream kernel would use 64-column blocks (128..255
@@ -915,6 +1064,15 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (K % 64 == 0) {
     kind = K_DMA_256x192;
   } else {
+    kind = K_TILE_128x128;
+  }
+  if (kind == K_ROWS) {
+    if (M <= 32 && K % 256 == 0 && rows_per_cu <= 48) {
+      p.kind = K_ROWS;
+      p.mf = M <= 16 ? 1 : 2;
+      p.bn = (int)rows_per_cu;
+      return p;
+    }
     kind = K_TILE_128x128;
   }
   if (kind == K_SKINNY) {
@@ -1043,10 +1201,25 @@ void launch_stream(const Plan& p, const int8_t* a, const int8_t* b, int M, int N
 #undef SI_STREAM
 }
 
+template <int MF, int EPI>
+void launch_rows(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
+                 const EpiArgs& ep, hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(N, p.bn));
+  const int G = (p.bn + 15) / 16;
+  if (G == 1) gemm_rows<MF, 1, 4, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+  else if (G == 2) gemm_rows<MF, 2, 4, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+  else gemm_rows<MF, 3, 4, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+}
+
 template <int EPI>
 void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K, int32_t* c,
             const EpiArgs& ep, hipStream_t st) {
   const dim3 block(256);
+  if (p.kind == K_ROWS) {
+    if (p.mf == 1) launch_rows<1, EPI>(p, a, b, M, N, K, c, ep, st);
+    else launch_rows<2, EPI>(p, a, b, M, N, K, c, ep, st);
+    return;
+  }
   if (p.kind == K_STREAM_N64 || p.kind == K_STREAM_N64_W8 || p.kind == K_STREAM_N32 ||
       p.kind == K_STREAM_N16 || p.kind == K_STREAM_N32_W8 || p.kind == K_STREAM_N16_W8) {
     switch (p.mf) {

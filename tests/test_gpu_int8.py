@@ -54,7 +54,11 @@ def _exact_i32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
                                    (7, 40, 24), (3, 17, 5), (100, 96, 48), (65, 4096, 200),
                                    (900, 1024, 300), (17, 11008, 4096), (16, 11008, 4096),
                                    (16, 4096, 22016), (3, 512, 5000), (20, 2048, 5),
-                                   (70, 4096, 33), (130, 11008, 7), (500, 2048, 100)])
+                                   (70, 4096, 33), (130, 11008, 7), (500, 2048, 100),
+                                   # one block per CU over ceil(N / 256) rows: ragged last
+                                   # block, one k stage, 48-row blocks, a 1-row last block
+                                   (1, 256, 4100), (31, 768, 6000), (32, 4096, 12288),
+                                   (9, 1280, 3841), (24, 512, 4096)])
 def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
     g = torch.Generator().manual_seed(M * 7 + K + N)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
