@@ -314,3 +314,31 @@ def test_step_and_copy_entry_points_reject_bad_arguments():
     assert lib.si_swiglu_quant(null, 2, 0, 64, null, null, null, null) == 0
     assert lib.si_rope_split(null, 2, 0, 8, 4, 64, null, null, null, null, null, null) == 0
     assert lib.si_kv_compact_flat(1, t16, t4, c5, t16, 0, 2, 1, 64, 16, 2, null) == 0
+
+
+def test_token_head_masks_follow_python_membership():
+    """The set / dict arguments of evict / apply_reuse_mask become a dense mask
+    by the reference's own rule: entry (t, h) is marked when ``(t, h) in items``
+    (a set) or ``items.get((t, h))`` is truthy (a dict), whatever the element
+    types (packed_kv_cache.py:679-687, 798-814). Both the host extension and the
+    item-by-item fallback are checked against that brute-force rule."""
+    import numpy as np
+    from shadowinfer_amd.shadowkv import _masks
+
+    S, H = 7, 3
+    items = {(0, 0), (1, 2), (True, False), (2.0, 1), (3.5, 1), (np.int64(4), np.int32(2)),
+             (6, 3), (-1, 0), (7, 0), (10 ** 30, 1), ("a", 1), (5,), (5, 1, 0), "x",
+             (float("nan"), 0), (np.float32(6.0), 0)}
+    as_dict = {k: (i % 3 != 0) for i, k in enumerate(sorted(items, key=repr))}
+    as_dict[(3, 0)] = 0
+    as_dict[(3, 1)] = "yes"
+    for container, is_dict in ((items, False), (frozenset(items), False), (as_dict, True)):
+        want = np.array([bool(container.get((t, h), False)) if is_dict else ((t, h) in container)
+                         for t in range(S) for h in range(H)], dtype=np.uint8)
+        got = _masks.token_head_mask(container, S, H, is_dict=is_dict)
+        got = np.zeros(S * H, np.uint8) if got is None else got
+        np.testing.assert_array_equal(got, want)
+        slow = np.zeros(S * H, np.uint8)
+        _masks._mark_python(container, S, H, slow, is_dict)
+        np.testing.assert_array_equal(slow, want)
+    assert _masks.token_head_mask(set(), S, H) is None
