@@ -342,3 +342,40 @@ def test_token_head_masks_follow_python_membership():
         _masks._mark_python(container, S, H, slow, is_dict)
         np.testing.assert_array_equal(slow, want)
     assert _masks.token_head_mask(set(), S, H) is None
+
+
+def test_map_to_codes_random_maps_match_the_dense_rule():
+    """The sparse host walk of map_to_codes against the oracle's dense grid
+    walk (precision_plan.py:30-55) on random maps whose keys are ints, floats,
+    bools, numpy integers and out-of-grid values, with mixed-case and unknown
+    names; the first unknown name in (token, head) order is the one reported.
+    codes_to_map inverts it exactly on random code matrices."""
+    import numpy as np
+    from shadowinfer_amd.shadowkv.precision_plan import codes_to_map, map_to_codes
+
+    rng = np.random.default_rng(11)
+    names = ["fp32", "FP16", "Int8", "int4", "evicted", "bf16", "fp8", 3, None]
+    for trial in range(40):
+        S, H = int(rng.integers(1, 12)), int(rng.integers(1, 6))
+        pm = {}
+        for _ in range(int(rng.integers(0, 2 * S))):
+            t = int(rng.integers(-2, S + 2))
+            tk = [t, float(t), np.int64(t)][int(rng.integers(0, 3))] if t != 1 else [1, True][int(rng.integers(0, 2))]
+            row = pm.setdefault(tk, {})
+            for _ in range(int(rng.integers(0, H + 2))):
+                h = int(rng.integers(-1, H + 1))
+                hk = [h, float(h) + [0.0, 0.5][int(rng.integers(0, 2))], np.int32(h)][int(rng.integers(0, 3))]
+                row[hk] = names[int(rng.integers(0, 5 if trial % 2 else len(names)))]
+        for strict in (True, False):
+            try:
+                want = O.map_to_codes(pm, S, H, strict=strict)
+            except ValueError as e:
+                with pytest.raises(ValueError) as got:
+                    map_to_codes(pm, S, H, strict=strict)
+                assert str(got.value) == str(e)
+                continue
+            np.testing.assert_array_equal(map_to_codes(pm, S, H, strict=strict).numpy(), want)
+        codes = rng.integers(0, 5, size=(S, H)).astype(np.int8)
+        back = codes_to_map(torch.from_numpy(codes))
+        assert list(back) == list(range(S)) and all(list(r) == list(range(H)) for r in back.values())
+        np.testing.assert_array_equal(map_to_codes(back, S, H).numpy(), codes)
