@@ -3,13 +3,17 @@
 Headline (``value``): KV pack+unpack throughput in GB/s over the 7B-shaped
 cache - 32 layers x B=1 x S=8192 x H=32 x D=128, bf16 K/V ~ N(0,1) with 1%
 outlier channels x8, precision codes 25% fp16 / 50% int8 / 25% int4 (group
-16) with a 4-token fp16 sink. One step = for every layer, pack (dense K/V ->
-precision buckets) then unpack (buckets -> fp32 K/V); inputs, plans and
-buckets are resident in HBM before the timed region. Before every launch the
-L2s and the Infinity Cache are flushed (a 512 MiB read, which leaves no dirty
-line behind), and each launch is timed alone with a HIP event pair on its
-stream; the step time is the sum.
-The same step back to back without flushes is reported as ``kv.warm_*``.
+16) with a 4-token fp16 sink. One step = pack every layer (dense K/V ->
+precision buckets), then unpack every layer (buckets -> fp32 K/V); inputs,
+plans and buckets are resident in HBM before the timed region. A layer's
+buckets are read back 31 launches after they were written and each K/V input
+63 launches after its last read, with at least 6.5 GB of other traffic in
+between (25x the 256 MB Infinity Cache plus the L2s), so every launch reads
+its inputs from HBM; the steps run back to back between two synchronizations,
+timed with HIP events on the launch stream.
+Beside it: ``kv.flushed_*``, the same launches each preceded by an explicit
+flush (a 512 MiB read, which leaves no dirty line behind) and timed alone
+with an event pair, and ``kv.warm_*``, each unpack right after its own pack.
 Throughput counts the algorithmic bytes: pack reads K+V and the code matrix
 and writes the packed bytes; unpack reads the packed bytes and the codes and
 writes fp32 K+V (slot metadata excluded).
@@ -123,7 +127,7 @@ def bench_kv(torch, dev, steps, warmup):
                      L["counts"], L["table"], L["sdt"], B, H, S, D, GROUP, L["ok"].data_ptr(),
                      L["ov"].data_ptr(), sptr)
 
-    def step():
+    def step_warm():  # each unpack right after its own layer's pack
         for L in layers:
             pack(L)
             unpack(L)
@@ -134,18 +138,53 @@ def bench_kv(torch, dev, steps, warmup):
     pack_bytes = [dense_in + codes_b + L["packed"] for L in layers]
     unpack_bytes = [L["packed"] + codes_b + fp32_out for L in layers]
     step_bytes = sum(pack_bytes) + sum(unpack_bytes)
+    avg_pack_b = sum(pack_bytes) / LAYERS
+    avg_unpack_b = sum(unpack_bytes) / LAYERS
 
+    # The headline: a step packs every layer, then unpacks every layer. A
+    # layer's buckets are read back 31 launches after they were written, and
+    # each K/V input 63 launches after its last read; between the two lie at
+    # least 6.5 GB of other traffic, 25x the 256 MB Infinity Cache plus the
+    # L2s, so no launch finds its inputs in a cache and every write-back of
+    # the step is paid inside it. `steps` steps run back to back between two
+    # synchronizations, timed by events on the launch stream; an event
+    # between the pack and the unpack half of every step gives each kernel's
+    # average launch time (32 launches per half, no event between them).
+    for _ in range(max(1, warmup)):
+        for L in layers:
+            pack(L)
+        for L in layers:
+            unpack(L)
+    torch.cuda.synchronize()
+    cev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for r in range(steps):
+        cev[r][0].record(stream)
+        for L in layers:
+            pack(L)
+        cev[r][1].record(stream)
+        for L in layers:
+            unpack(L)
+        cev[r][2].record(stream)
+    torch.cuda.synchronize()
+    c_wall = (time.perf_counter() - t0) / steps * 1e3
+    c_step = cev[0][0].elapsed_time(cev[-1][2]) / steps
+    c_pack = sum(e[0].elapsed_time(e[1]) for e in cev) / (steps * LAYERS)
+    c_unpack = sum(e[1].elapsed_time(e[2]) for e in cev) / (steps * LAYERS)
+
+    # The same step with each unpack right after its own pack (its buckets
+    # partly still in the Infinity Cache): reported as warm_*.
     for _ in range(warmup):
-        step()
+        step_warm()
     torch.cuda.synchronize()
     timer = EventTimer(torch, stream)
     t0 = time.perf_counter()
-    ms_step = timer.time(step, steps)
+    ms_step = timer.time(step_warm, steps)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
 
-    # Per-launch durations inside the same step loop: an event pair around
-    # every pack and every unpack launch, on the launch stream.
+    # Per-launch durations inside that warm loop: an event pair around every
+    # pack and every unpack launch, on the launch stream.
     reps = max(2, steps // 4)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(LAYERS * reps)]
     for r in range(reps):
@@ -159,37 +198,34 @@ def bench_kv(torch, dev, steps, warmup):
     torch.cuda.synchronize()
     ms_pack = sum(e0.elapsed_time(e1) for e0, e1, _ in evs) / len(evs)
     ms_unpack = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / len(evs)
-    avg_pack_b = sum(pack_bytes) / LAYERS
-    avg_unpack_b = sum(unpack_bytes) / LAYERS
 
-    # Flushed protocol (the headline): before every pack and every unpack
-    # launch a FLUSH_BYTES buffer is read in full (a sum), which replaces the
-    # contents of the 256 MB Infinity Cache and of every L2 with clean lines,
-    # so each launch reads its inputs from HBM and no earlier write is still
-    # waiting to be written back (a flush by overwriting would leave that
-    # write-back to the timed launch); each launch is timed alone with an
-    # event pair on its stream. A step is the 32 packs and 32 unpacks; its
-    # time is the sum of their launch times.
+    # Explicit flushes: before every pack and every unpack launch a
+    # FLUSH_BYTES buffer is read in full (a sum), which replaces the contents
+    # of the Infinity Cache and of every L2 with clean lines, so each launch
+    # reads its inputs from HBM and no earlier write is still waiting to be
+    # written back (a flush by overwriting would leave that write-back to the
+    # timed launch); each launch is timed alone with an event pair, which
+    # adds its dispatch gap. Reported as flushed_*.
     flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
 
-    def flush(i):
+    def flush():
         flush_buf.sum(dtype=torch.int64)
 
-    for i, L in enumerate(layers[:2]):
-        flush(i)
+    for L in layers[:2]:
+        flush()
         pack(L)
-        flush(i + 1)
+        flush()
         unpack(L)
     fev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(LAYERS * steps)]
     torch.cuda.synchronize()
     for r in range(steps):
         for i, L in enumerate(layers):
             e = fev[r * LAYERS + i]
-            flush(2 * i)
+            flush()
             e[0].record(stream)
             pack(L)
             e[1].record(stream)
-            flush(2 * i + 1)
+            flush()
             e[2].record(stream)
             unpack(L)
             e[3].record(stream)
@@ -201,19 +237,28 @@ def bench_kv(torch, dev, steps, warmup):
     fu = sum(f_unpack) / len(f_unpack)
     del flush_buf
     res = {
-        "protocol": f"caches flushed (a {FLUSH_BYTES >> 20} MiB read) before every launch; "
-                    "each launch timed alone with an event pair",
-        "ms_per_step": f_step_ms,
+        "protocol": "each step packs all 32 layers, then unpacks them: a layer's buckets are "
+                    "read back 31 launches (>= 6.5 GB of traffic) after they were written, every "
+                    "K/V input 63 launches after its last read; steps timed back to back",
+        "ms_per_step": c_step,
+        "wall_ms_per_step": c_wall,
         "step_bytes": step_bytes,
-        "gbs": step_bytes / (f_step_ms * 1e-3) / 1e9,
-        "pack_us": fp * 1e3,
-        "unpack_us": fu * 1e3,
-        "pack_gbs": avg_pack_b / (fp * 1e-3) / 1e9,
-        "unpack_gbs": avg_unpack_b / (fu * 1e-3) / 1e9,
+        "gbs": step_bytes / (c_step * 1e-3) / 1e9,
+        "pack_us": c_pack * 1e3,
+        "unpack_us": c_unpack * 1e3,
+        "pack_gbs": avg_pack_b / (c_pack * 1e-3) / 1e9,
+        "unpack_gbs": avg_unpack_b / (c_unpack * 1e-3) / 1e9,
         "pack_bytes_per_launch": avg_pack_b,
         "unpack_bytes_per_launch": avg_unpack_b,
         "packed_bytes_per_layer": sum(L["packed"] for L in layers) / LAYERS,
-        # back to back, no flush: each unpack follows its own layer's pack
+        # explicit 512 MiB flush read before every launch, each launch timed alone
+        "flushed_ms_per_step": f_step_ms,
+        "flushed_gbs": step_bytes / (f_step_ms * 1e-3) / 1e9,
+        "flushed_pack_us": fp * 1e3,
+        "flushed_unpack_us": fu * 1e3,
+        "flushed_pack_gbs": avg_pack_b / (fp * 1e-3) / 1e9,
+        "flushed_unpack_gbs": avg_unpack_b / (fu * 1e-3) / 1e9,
+        # back to back, each unpack right after its own layer's pack
         "warm_ms_per_step": ms_step,
         "warm_wall_ms_per_step": wall,
         "warm_gbs": step_bytes / (ms_step * 1e-3) / 1e9,
@@ -852,8 +897,8 @@ def main():
         return
     log("kv pack+unpack")
     kv = bench_kv(torch, dev, args.steps, args.warmup)
-    log(f"kv flushed {kv['gbs']:.1f} GB/s (pack {kv['pack_us']:.1f} us, unpack "
-        f"{kv['unpack_us']:.1f} us); warm {kv['warm_gbs']:.1f} GB/s")
+    log(f"kv {kv['gbs']:.1f} GB/s (pack {kv['pack_us']:.1f} us, unpack {kv['unpack_us']:.1f} us); "
+        f"flushed per launch {kv['flushed_gbs']:.1f} GB/s; warm {kv['warm_gbs']:.1f} GB/s")
     gemm = attn = adm = paged = step = None
     if args.part == "all":
         log("int8 gemm")
@@ -898,7 +943,8 @@ def main():
                         "bf16 K/V, codes 25% fp16 / 50% int8 / 25% int4 g16, 4-token fp16 sink",
             "layers": LAYERS, "batch": B, "seq_len": S, "heads": H, "head_dim": D,
             "int4_group": GROUP, "hbm_frac": round(kv["gbs"] / HBM_PEAK_GBS, 4),
-            "protocol": "caches flushed before every pack and unpack launch",
+            "protocol": "pack all 32 layers, then unpack them; each launch's inputs last "
+                        "touched >= 6.5 GB of traffic earlier (cold); steps timed back to back",
         },
         "roofline": {
             "kernel": f"kv_{dom}",
