@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SI_ABI_VERSION 3
+#define SI_ABI_VERSION 4
 
 #define SI_OK 0
 #define SI_ERR_INVALID 1
@@ -295,6 +295,15 @@ int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t* b, const 
                        int out_dtype, void* workspace, size_t workspace_bytes,
                        si_stream_t stream);
 
+/* si_gemm_i8_dequant followed by the decoder layer's residual add
+ * (models/diffusion_llama.py:421-423, hidden = residual + mlp(...)):
+ * out = T(residual + T(float(acc) * (sx * sw) [+ bias])), residual [M, N] in
+ * out_dtype. out may be the residual buffer itself (an in-place add). */
+int si_gemm_i8_dequant_add(const int8_t* a, const float* sx, const int8_t* b, const float* sw,
+                           const float* bias, const void* residual, int64_t M, int64_t N,
+                           int64_t K, void* out, int out_dtype, void* workspace,
+                           size_t workspace_bytes, si_stream_t stream);
+
 /* Workspace bytes of si_int8_linear_forward (quantized activations, their
  * scales and the GEMM workspace). */
 size_t si_int8_linear_workspace_bytes(int64_t M, int64_t K, int64_t N);
@@ -306,6 +315,15 @@ int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64_t K, int64
                            const int8_t* qweight, const float* sw, const float* bias,
                            void* out, void* workspace, size_t workspace_bytes,
                            si_stream_t stream);
+
+/* si_int8_linear_forward followed by the residual add of the decoder layer
+ * (diffusion_llama.py:421-423): out = T(residual + T(INT8Linear(x))),
+ * residual [M, N] in dtype; out may be the residual buffer itself. Same
+ * workspace as si_int8_linear_forward. */
+int si_int8_linear_forward_add(const void* x, int dtype, int64_t M, int64_t K, int64_t N,
+                               const int8_t* qweight, const float* sw, const float* bias,
+                               const void* residual, void* out, void* workspace,
+                               size_t workspace_bytes, si_stream_t stream);
 
 /* Size of the device scratch array of si_int8_linear_forward_noalloc (one
  * per device, held until the process ends). */

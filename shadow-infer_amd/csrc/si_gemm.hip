@@ -38,7 +38,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-enum Epi { EPI_I32 = 0, EPI_PARTIAL = 1, EPI_DEQUANT = 2 };
+enum Epi { EPI_I32 = 0, EPI_PARTIAL = 1, EPI_DEQUANT = 2, EPI_RESID = 256 };
 
 struct EpiArgs {
   const float* sx;
@@ -48,15 +48,32 @@ struct EpiArgs {
   int out_dtype;
   int32_t* partial;  // [splits, M, N] when EPI_PARTIAL
   int vec;           // 16-byte stores allowed: N % 8 == 0 and every output/scale pointer aligned
+  const void* resid; // [M, N] in the output dtype, or null: out = T(resid + T(projection))
 };
 
-// out = T(float(acc) * (sx * sw) [+ bias]) with the reference's rounding order.
+// The residual add that follows a projection in the reference's decoder layer
+// (models/diffusion_llama.py:421-423): the INT8Linear output is rounded to the
+// output dtype T (int8_linear.py:115), then added to the residual stream in T.
+// The caller's store rounds the sum to T. `out` may alias `resid`: every
+// element is read by the thread that writes it, before the write.
+template <int ODT>
+__device__ __forceinline__ float add_resid(const EpiArgs& ep, int64_t idx, float o) {
+  if (ep.resid == nullptr) return o;
+  return round_to(o, ODT) + load_any(ep.resid, ODT, idx);
+}
+__device__ __forceinline__ float add_resid_rt(const EpiArgs& ep, int64_t idx, float o) {
+  if (ep.resid == nullptr) return o;
+  return round_to(o, ep.out_dtype) + load_any(ep.resid, ep.out_dtype, idx);
+}
+
+// out = T(float(acc) * (sx * sw) [+ bias]) with the reference's rounding order
+// (then the residual add when ep.resid is set).
 __device__ __forceinline__ void store_dequant(const EpiArgs& ep, int64_t idx, int32_t acc, float sx,
                                               float sw, float bias) {
   const float sc = sx * sw;
   float o = (float)acc * sc;
   if (ep.bias != nullptr) o = o + bias;
-  store_any(ep.out, ep.out_dtype, idx, o);
+  store_any(ep.out, ep.out_dtype, idx, add_resid_rt(ep, idx, o));
 }
 
 template <int EPI>
@@ -170,7 +187,8 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
   }
 }
 
-// EPI: EPI_I32 / EPI_PARTIAL; EPI_DEQUANT + 16 * out dtype for the dequant epilogue.
+// EPI: EPI_I32 / EPI_PARTIAL; EPI_DEQUANT + 16 * out dtype for the dequant
+// epilogue, + EPI_RESID when a residual is added (ep.resid set).
 template <int BM, int BN, int BK, int WM, int WN, int EPI>
 __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ B, int M, int N, int K,
@@ -223,7 +241,7 @@ __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
   const int col = lane & 31;
   const int rq = (lane >> 5) * 4;
   constexpr int KIND = EPI & 15;
-  constexpr int ODT = EPI >> 4;
+  constexpr int ODT = (EPI >> 4) & 15;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int n = n0 + wn * TN + j * 32 + col;
@@ -248,6 +266,7 @@ __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
         } else {
           float o = (float)v * (ep.sx[m] * sw);
           if (ep.bias != nullptr) o = o + bias;
+          if constexpr ((EPI & EPI_RESID) != 0) o = add_resid<ODT>(ep, idx, o);
           store_out<ODT>(ep.out, idx, o);
         }
       }
@@ -326,6 +345,24 @@ __device__ __forceinline__ int xcd_order(int b, int n) {
   return x < tall ? x * per + j : tall * per + (x - tall) * (per - 1) + j;
 }
 
+// 8 consecutive values of type ODT at element idx (16- or 32-byte aligned).
+template <int ODT>
+__device__ __forceinline__ void load8_out(const void* p, int64_t idx, float* r) {
+  if constexpr (ODT == SI_DT_F32) {
+    const float4 a = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + idx)[0];
+    const float4 b = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + idx)[1];
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w; r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + idx);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[2 * e] = ODT == SI_DT_BF16 ? bf16_bits_to_f32(ws[e] & 0xffffu) : f16_bits_to_f32(ws[e] & 0xffffu);
+      r[2 * e + 1] = ODT == SI_DT_BF16 ? bf16_bits_to_f32(ws[e] >> 16) : f16_bits_to_f32(ws[e] >> 16);
+    }
+  }
+}
+
 template <int ODT>
 __device__ __forceinline__ void store8(void* out, int64_t idx, const float* o) {
   if constexpr (ODT == SI_DT_F32) {
@@ -349,15 +386,50 @@ __device__ __forceinline__ void store8(void* out, int64_t idx, const float* o) {
 // is EPI_DEQUANT + 16 * output dtype). Accumulator register r of a fragment
 // holds row 8*(r/4) + 4*(lane/32) + r%4, column lane%32, so registers
 // [8h, 8h+8) hold rows 16h .. 16h+15.
+// Residual chunks of one band for one lane: for pass h and chunk slot s, the 8
+// values at the element store_frag_row writes there (loaded before any store
+// of the tile, so their latency is paid once per tile; each element is read
+// by the lane that later writes it, so `out` may alias the residual).
+template <int FN>
+struct BandResid {
+  static constexpr int CPL = (16 * (32 * FN / 8) + 63) / 64;  // chunks per lane per pass
+  uint4 r[2][CPL];
+};
+
+template <int FN, int ODT>
+__device__ __forceinline__ void load_band_resid(BandResid<FN>& br, int m_base, int n_base,
+                                                int lane, int M, int N, const EpiArgs& ep) {
+  constexpr int CH = 32 * FN / 8;
+  constexpr int CPL = BandResid<FN>::CPL;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) {
+      const int c = lane + 64 * s;
+      const int m = m_base + 16 * h + c / CH;
+      const int n = n_base + (c % CH) * 8;
+      br.r[h][s] = make_uint4(0, 0, 0, 0);
+      if (c < 16 * CH && m < M && ep.vec && n + 8 <= N) {
+        const int64_t idx = (int64_t)m * N + n;
+        if constexpr (ODT == SI_DT_F32) {
+          // two halves of 32 bytes do not fit a uint4: the fp32 path reads in the store loop
+        } else {
+          br.r[h][s] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(ep.resid) + idx);
+        }
+      }
+    }
+}
+
 template <int FN, int EPI>
 __device__ __forceinline__ void store_frag_row(const v16i* acc, int m_base, int n_base, int32_t* stg,
                                                int lane, int M, int N, int32_t* dst,
-                                               const EpiArgs& ep) {
+                                               const EpiArgs& ep, const BandResid<FN>* br) {
   constexpr int TN = 32 * FN;
   constexpr int EP = TN + 8;  // staging pitch in words (rows r and r+4 on other banks)
   constexpr int CH = TN / 8;  // 8-wide chunks per staged row
   constexpr int KIND = EPI & 15;
-  constexpr int ODT = EPI >> 4;
+  constexpr int ODT = (EPI >> 4) & 15;
+  constexpr bool RES = (EPI & EPI_RESID) != 0;
   const int col = lane & 31;
   const int rq = (lane >> 5) * 4;
 #pragma unroll
@@ -370,7 +442,9 @@ __device__ __forceinline__ void store_frag_row(const v16i* acc, int m_base, int 
     wait_cnt<63, 0>();
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int c = lane; c < 16 * CH; c += 64) {
+    for (int s = 0; s < BandResid<FN>::CPL; ++s) {
+      const int c = lane + 64 * s;
+      if (c >= 16 * CH) continue;
       const int row = c / CH;
       const int ch = c % CH;
       const int m = m_base + 16 * h + row;
@@ -405,11 +479,28 @@ __device__ __forceinline__ void store_frag_row(const v16i* acc, int m_base, int 
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = o[e] + bb[e];
           }
+          if constexpr (RES) {
+            float r[8];
+            if constexpr (ODT == SI_DT_F32) {
+              load8_out<ODT>(ep.resid, idx, r);
+            } else {
+              const uint4 w = br->r[h][s];
+              const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                r[2 * e] = ODT == SI_DT_BF16 ? bf16_bits_to_f32(ws[e] & 0xffffu) : f16_bits_to_f32(ws[e] & 0xffffu);
+                r[2 * e + 1] = ODT == SI_DT_BF16 ? bf16_bits_to_f32(ws[e] >> 16) : f16_bits_to_f32(ws[e] >> 16);
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = round_to(o[e], ODT) + r[e];
+          }
           store8<ODT>(ep.out, idx, o);
         } else {
           for (int e = 0; e < 8 && n + e < N; ++e) {
             float x = (float)v[e] * (sx * ep.sw[n + e]);
             if (ep.bias != nullptr) x = x + ep.bias[n + e];
+            if constexpr (RES) x = add_resid<ODT>(ep, idx + e, x);
             store_out<ODT>(ep.out, idx + e, x);
           }
         }
@@ -568,9 +659,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
   __syncthreads();  // every wave is done with the stages
   int32_t* stg = reinterpret_cast<int32_t*>(lds) + wave * (16 * EP);
   int32_t* dst = (EPI & 15) == EPI_PARTIAL ? ep.partial + (int64_t)split * M * N : Cout;
+  if constexpr ((EPI & EPI_RESID) != 0) {
+    BandResid<FN> br[FM];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
-    store_frag_row<FN, EPI>(acc[i], m0 + wm * TM + i * 32, n0 + wn * TN, stg, lane, M, N, dst, ep);
+    for (int i = 0; i < FM; ++i)
+      load_band_resid<FN, (EPI >> 4) & 15>(br[i], m0 + wm * TM + i * 32, n0 + wn * TN, lane, M, N, ep);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      store_frag_row<FN, EPI>(acc[i], m0 + wm * TM + i * 32, n0 + wn * TN, stg, lane, M, N, dst,
+                              ep, &br[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      store_frag_row<FN, EPI>(acc[i], m0 + wm * TM + i * 32, n0 + wn * TN, stg, lane, M, N, dst,
+                              ep, nullptr);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -884,7 +987,8 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
       if (EPI == EPI_DEQUANT) {
         float o = (float)v * (esx[x] * esw[x]);
         if (ep.bias != nullptr) o = o + eb[x];
-        store_any(ep.out, ep.out_dtype, (int64_t)m * N + n0 + jj, o);
+        const int64_t idx = (int64_t)m * N + n0 + jj;
+        store_any(ep.out, ep.out_dtype, idx, add_resid_rt(ep, idx, o));
       } else {
         epi_store<EPI>(ep, C, M, N, m, n0 + jj, v, 0);
       }
@@ -1242,6 +1346,13 @@ void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K
   }
   if (EPI != EPI_DEQUANT) {
     launch_tile<EPI>(p, a, b, M, N, K, c, ep, st);
+  } else if (ep.resid != nullptr) {
+    if (ep.out_dtype == SI_DT_F32)
+      launch_tile<EPI_DEQUANT + 16 * SI_DT_F32 + EPI_RESID>(p, a, b, M, N, K, c, ep, st);
+    else if (ep.out_dtype == SI_DT_F16)
+      launch_tile<EPI_DEQUANT + 16 * SI_DT_F16 + EPI_RESID>(p, a, b, M, N, K, c, ep, st);
+    else
+      launch_tile<EPI_DEQUANT + 16 * SI_DT_BF16 + EPI_RESID>(p, a, b, M, N, K, c, ep, st);
   } else if (ep.out_dtype == SI_DT_F32) {
     launch_tile<EPI_DEQUANT + 16 * SI_DT_F32>(p, a, b, M, N, K, c, ep, st);
   } else if (ep.out_dtype == SI_DT_F16) {
@@ -1258,7 +1369,7 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
   {
     uintptr_t bits = reinterpret_cast<uintptr_t>(c) | reinterpret_cast<uintptr_t>(ep.out) |
                      reinterpret_cast<uintptr_t>(ep.sw) | reinterpret_cast<uintptr_t>(ep.bias) |
-                     reinterpret_cast<uintptr_t>(ws);
+                     reinterpret_cast<uintptr_t>(ep.resid) | reinterpret_cast<uintptr_t>(ws);
     ep.vec = (N % 8 == 0 && (bits & 15) == 0) ? 1 : 0;
   }
   if (p.kind == K_SCALAR) {
@@ -1314,20 +1425,41 @@ extern "C" int si_gemm_i8i8_i32(const int8_t* a, const int8_t* b, int64_t M, int
                   "si_gemm_i8i8_i32");
 }
 
+namespace {
+int gemm_dequant(const int8_t* a, const float* sx, const int8_t* b, const float* sw,
+                 const float* bias, const void* resid, int64_t M, int64_t N, int64_t K, void* out,
+                 int out_dtype, void* workspace, size_t workspace_bytes, si_stream_t stream,
+                 const char* who) {
+  SI_CHECK_ARG(dtype_ok(out_dtype), "%s: unsupported out dtype %d", who, out_dtype);
+  SI_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "%s: bad shape", who);
+  if (M == 0 || N == 0) return SI_OK;
+  SI_CHECK_ARG(a && sx && b && sw && out, "%s: NULL argument", who);
+  SI_CHECK_ARG(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0,
+               "%s: operands must be 16-byte aligned", who);
+  EpiArgs ep{sx, sw, bias, out, out_dtype, nullptr, 0, resid};
+  return run_gemm(a, b, M, N, K, nullptr, ep, true, workspace, workspace_bytes,
+                  as_stream(stream), who);
+}
+}  // namespace
+
 extern "C" int si_gemm_i8_dequant(const int8_t* a, const float* sx, const int8_t* b,
                                   const float* sw, const float* bias, int64_t M, int64_t N,
                                   int64_t K, void* out, int out_dtype, void* workspace,
                                   size_t workspace_bytes, si_stream_t stream) {
   clear_error();
-  SI_CHECK_ARG(dtype_ok(out_dtype), "si_gemm_i8_dequant: unsupported out dtype %d", out_dtype);
-  SI_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "si_gemm_i8_dequant: bad shape");
-  if (M == 0 || N == 0) return SI_OK;
-  SI_CHECK_ARG(a && sx && b && sw && out, "si_gemm_i8_dequant: NULL argument");
-  SI_CHECK_ARG(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0,
-               "si_gemm_i8_dequant: operands must be 16-byte aligned");
-  EpiArgs ep{sx, sw, bias, out, out_dtype, nullptr};
-  return run_gemm(a, b, M, N, K, nullptr, ep, true, workspace, workspace_bytes,
-                  as_stream(stream), "si_gemm_i8_dequant");
+  return gemm_dequant(a, sx, b, sw, bias, nullptr, M, N, K, out, out_dtype, workspace,
+                      workspace_bytes, stream, "si_gemm_i8_dequant");
+}
+
+extern "C" int si_gemm_i8_dequant_add(const int8_t* a, const float* sx, const int8_t* b,
+                                      const float* sw, const float* bias, const void* residual,
+                                      int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
+                                      void* workspace, size_t workspace_bytes,
+                                      si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(residual != nullptr || M == 0 || N == 0, "si_gemm_i8_dequant_add: NULL residual");
+  return gemm_dequant(a, sx, b, sw, bias, residual, M, N, K, out, out_dtype, workspace,
+                      workspace_bytes, stream, "si_gemm_i8_dequant_add");
 }
 
 extern "C" size_t si_int8_linear_workspace_bytes(int64_t M, int64_t K, int64_t N) {
@@ -1358,6 +1490,30 @@ extern "C" int si_int8_linear_forward(const void* x, int dtype, int64_t M, int64
   if (int rc = si_act_quant_i8(x, dtype, M, K, q, sx, stream)) return rc;
   return si_gemm_i8_dequant(q, sx, qweight, sw, bias, M, N, K, out, dtype, gws,
                             workspace_bytes - qbytes - sbytes, stream);
+}
+
+extern "C" int si_int8_linear_forward_add(const void* x, int dtype, int64_t M, int64_t K, int64_t N,
+                                          const int8_t* qweight, const float* sw,
+                                          const float* bias, const void* residual, void* out,
+                                          void* workspace, size_t workspace_bytes,
+                                          si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(dtype), "si_int8_linear_forward_add: unsupported dtype %d", dtype);
+  SI_CHECK_ARG(M >= 0 && K > 0 && N > 0, "si_int8_linear_forward_add: bad shape");
+  if (M == 0) return SI_OK;
+  SI_CHECK_ARG(x && qweight && sw && out && residual, "si_int8_linear_forward_add: NULL argument");
+  const size_t need = si_int8_linear_workspace_bytes(M, K, N);
+  SI_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+               "si_int8_linear_forward_add: workspace too small (%zu < %zu bytes)",
+               workspace_bytes, need);
+  int8_t* q = reinterpret_cast<int8_t*>(workspace);
+  const size_t qbytes = ((size_t)M * (size_t)K + 255) & ~(size_t)255;
+  float* sx = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + qbytes);
+  const size_t sbytes = ((size_t)M * sizeof(float) + 255) & ~(size_t)255;
+  void* gws = reinterpret_cast<char*>(workspace) + qbytes + sbytes;
+  if (int rc = si_act_quant_i8(x, dtype, M, K, q, sx, stream)) return rc;
+  return gemm_dequant(q, sx, qweight, sw, bias, residual, M, N, K, out, dtype, gws,
+                      workspace_bytes - qbytes - sbytes, stream, "si_int8_linear_forward_add");
 }
 
 // ---------------------------------------------------------------------------

@@ -83,6 +83,8 @@ _SIGNATURES = {
     "si_gemm_i8i8_i32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "si_gemm_i8_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp,
                                   _sz, _vp]),
+    "si_gemm_i8_dequant_add": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32,
+                                      _vp, _sz, _vp]),
     "si_kv_sensitivity": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp]),
     "si_admit_workspace_bytes": (_sz, [_i64]),
     "si_admit_codes": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
@@ -99,6 +101,8 @@ _SIGNATURES = {
     "si_int8_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "si_int8_linear_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                       _sz, _vp]),
+    "si_int8_linear_forward_add": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, _sz, _vp]),
     "si_int8_linear_forward_noalloc": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                               _vp]),
 }

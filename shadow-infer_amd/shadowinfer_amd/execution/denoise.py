@@ -27,7 +27,7 @@ attention writing token-major output (HIP) -> o projection (bf16 library
 GEMM) -> residual add fused with the RMSNorm and the activation quantization
 (HIP) -> gate|up INT8 GEMM (HIP, one GEMM over both weights) ->
 SwiGLU fused with the down projection's activation quantization (HIP) ->
-down INT8 GEMM (HIP) -> residual add.
+down INT8 GEMM with the residual add in its epilogue (HIP).
 
 Weights are random (no checkpoints are loaded): linear weights ~ N(0, 0.02),
 norms = 1, as a Llama initializer would give.
@@ -168,8 +168,11 @@ class PackedDiffusionLlama:
                                          want_q=True, residual=o)
         gu = row_ops.int8_gemm_dequant(qx, sx, L.gu_q, L.gu_s, self.dtype)
         h, qh, sh = row_ops.swiglu_quant(gu, want_h=trace is not None)
-        ffn = row_ops.int8_gemm_dequant(qh, sh, L.dn_q, L.dn_s, self.dtype)
-        out = x1 + ffn
+        # the down projection with the residual add in its epilogue
+        out = row_ops.int8_gemm_dequant(qh, sh, L.dn_q, L.dn_s, self.dtype, residual=x1)
+        ffn = None
+        if trace is not None:
+            ffn = row_ops.int8_gemm_dequant(qh, sh, L.dn_q, L.dn_s, self.dtype)
         if trace is not None:
             trace.update(x=x, xn=xn, qkv=qkv, q=q, k=k, v=v, cache=cache, attn=attn, o=o, x1=x1,
                          y2=y2, qx=qx, sx=sx, gu=gu, h=h, qh=qh, sh=sh, ffn=ffn, out=out)

@@ -94,9 +94,13 @@ def swiglu_quant(gate_up: torch.Tensor, want_h: bool = False
 
 def int8_gemm_dequant(q: torch.Tensor, sx: torch.Tensor, qweight_nk: torch.Tensor,
                       sw: torch.Tensor, out_dtype: torch.dtype,
-                      bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      bias: Optional[torch.Tensor] = None,
+                      residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """INT8Linear.forward after its prologue (int8_linear.py:102-115):
-    ``T(float(q @ qweight_nk^T) * (sx[m] * sw[n]) [+ bias])``."""
+    ``T(float(q @ qweight_nk^T) * (sx[m] * sw[n]) [+ bias])``; with
+    ``residual`` (``[M, N]`` in ``out_dtype``) the decoder layer's residual add
+    follows in the same pass: ``T(residual + T(...))``
+    (models/diffusion_llama.py:421-423)."""
     _native.require_device(q, "int8_gemm_dequant")
     M, K = q.shape
     N = qweight_nk.shape[0]
@@ -105,8 +109,16 @@ def int8_gemm_dequant(q: torch.Tensor, sx: torch.Tensor, qweight_nk: torch.Tenso
     out = torch.empty(M, N, dtype=out_dtype, device=q.device)
     ws_bytes = _native.size_query("si_gemm_workspace_bytes", M, N, K)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
-    _native.call("si_gemm_i8_dequant", q.data_ptr(), sx.data_ptr(), qweight_nk.data_ptr(),
-                 sw.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
+    if residual is None:
+        _native.call("si_gemm_i8_dequant", q.data_ptr(), sx.data_ptr(), qweight_nk.data_ptr(),
+                     sw.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
+                     _native.dtype_code(out_dtype), _ptr(ws), ws_bytes, _native.stream(q.device))
+        return out
+    if residual.shape != (M, N) or residual.dtype != out_dtype or not residual.is_contiguous():
+        raise ValueError(f"residual must be a contiguous [{M}, {N}] {out_dtype} tensor, got "
+                         f"{tuple(residual.shape)} {residual.dtype}")
+    _native.call("si_gemm_i8_dequant_add", q.data_ptr(), sx.data_ptr(), qweight_nk.data_ptr(),
+                 sw.data_ptr(), _ptr(bias), residual.data_ptr(), M, N, K, out.data_ptr(),
                  _native.dtype_code(out_dtype), _ptr(ws), ws_bytes, _native.stream(q.device))
     return out
 

@@ -342,3 +342,67 @@ def test_int4_all_nibble_pairs(dev):
     packed = Quantizer.pack_int4(t.to(dev)).cpu()
     expected = ((hi.reshape(-1) + 8) << 4) | (lo.reshape(-1) + 8)
     assert torch.equal(packed.to(torch.int64), expected)
+
+
+# --- the down projection's residual add fused into the epilogue ------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("M,K,N,bias", [(16, 4096, 11008, False), (8, 320, 3000, True),
+                                        (64, 4096, 11008, False), (48, 11008, 4096, True),
+                                        (300, 512, 272, True), (5, 40, 24, False),
+                                        (128, 4000, 300, False)])
+def test_gemm_dequant_add_bit_exact(dev, dtype, M, K, N, bias):
+    """si_gemm_i8_dequant_add = T(residual + T(acc * (sx * sw) [+ bias])), the
+    INT8Linear output rounded to T and added to the residual stream in T
+    (diffusion_llama.py:421-423), on shapes that reach the row-streaming,
+    weight-streaming, 64x64, split-K, large-tile, register-staged and scalar
+    kernels; also in place (out is the residual buffer)."""
+    from oracle import denoise_ref as R
+    g = torch.Generator().manual_seed(M + 3 * K + N)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    b = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sx = torch.rand(M, generator=g) * 0.05 + 1e-3
+    sw = torch.rand(N, generator=g) * 1e-3 + 1e-5
+    bs = torch.randn(N, generator=g) if bias else None
+    resid = (torch.randn(M, N, generator=g) * 4).to(dtype)
+    dt = DT[dtype]
+    ffn = O.int8_epilogue(O.gemm_i8(a.numpy(), b.numpy().T), sx.numpy(), sw.numpy(),
+                          None if bs is None else bs.numpy(), dt)
+    want = R.add(to_np(resid), ffn, dt)
+    ad, bd, sxd, swd = a.to(dev), b.to(dev), sx.to(dev), sw.to(dev)
+    bsd = None if bs is None else bs.to(dev)
+    ws_bytes = _native.size_query("si_gemm_workspace_bytes", M, N, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    rd = resid.to(dev)
+    for in_place in (False, True):
+        out = rd.clone() if in_place else torch.empty(M, N, dtype=dtype, device=dev)
+        src = out if in_place else rd
+        _native.call("si_gemm_i8_dequant_add", ad.data_ptr(), sxd.data_ptr(), bd.data_ptr(),
+                     swd.data_ptr(), _native.ptr(bsd), src.data_ptr(), M, N, K, out.data_ptr(),
+                     _native.dtype_code(dtype), ws.data_ptr(), ws_bytes, _native.stream(dev))
+        np.testing.assert_array_equal(to_np(out), want)
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 11008), (64, 128, 96), (2048, 11008, 4096)])
+def test_int8_linear_forward_add_bit_exact(dev, M, K, N):
+    """si_int8_linear_forward_add: the whole INT8Linear forward (activation
+    quantization, GEMM, epilogue) then the residual add, bf16."""
+    from oracle import denoise_ref as R
+    torch.manual_seed(M + K)
+    lin = nn.Linear(K, N, bias=(M == 64))
+    layer = INT8Linear.from_linear(lin.to(dev))
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    resid = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    ref, _, _, _ = O.int8_linear_forward(to_np(x), O.BF16, layer.qweight.cpu().numpy(),
+                                         layer.weight_scale.cpu().numpy(),
+                                         None if layer.bias is None else layer.bias.cpu().numpy())
+    want = R.add(to_np(resid), ref, O.BF16)
+    xd, rd = x.to(dev), resid.to(dev)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ws_bytes = _native.size_query("si_int8_linear_workspace_bytes", M, K, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _native.call("si_int8_linear_forward_add", xd.data_ptr(), _native.DT_BF16, M, K, N,
+                 layer.qweight_nk.data_ptr(), layer.weight_scale.data_ptr(),
+                 _native.ptr(layer.bias), rd.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                 _native.stream(dev))
+    np.testing.assert_array_equal(to_np(out), want)
