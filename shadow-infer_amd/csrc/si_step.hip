@@ -90,8 +90,11 @@ __device__ __forceinline__ void store8(void* p, int64_t i, const float* v) {
 }
 
 // INT8Linear activation quantization of a row held by the block
-// (int8_linear.py:96-98): s = max(amax / 127, 1e-8), q = clamp(rint(x / s), +-127),
-// IEEE division, as si_act_quant_i8.
+// (int8_linear.py:96-98): s = max(amax / 127, 1e-8), q = clamp(rint(x / s), +-127)
+// with the IEEE quotient, as si_act_quant_i8.
+// The quotient is Markstein's: q0 = x * r with r = RN(1/s), e = x - q0 * s
+// (exact, one fma), q1 = RN(q0 + e * r) = RN(x/s) for every finite x and
+// normal s (s >= 1e-8 here) -- the IEEE quotient without a division per value.
 template <int R>
 __device__ __forceinline__ void quant_row(float (&v)[R][8], int nch, int64_t row, int K,
                                           int8_t* __restrict__ q, float* __restrict__ scale,
@@ -106,6 +109,7 @@ __device__ __forceinline__ void quant_row(float (&v)[R][8], int nch, int64_t row
   float s = a / 127.0f;
   s = s < 1e-8f ? 1e-8f : s;  // clamp_min(1e-8); NaN passes through like torch
   if (threadIdx.x == 0) scale[row] = s;
+  const float rinv = 1.0f / s;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int c = (int)threadIdx.x + r * 256;
@@ -113,12 +117,27 @@ __device__ __forceinline__ void quant_row(float (&v)[R][8], int nch, int64_t row
     uint32_t b[2] = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float t = rintf(v[r][e] / s);
+      const float q0 = v[r][e] * rinv;
+      float t = rintf(__builtin_fmaf(__builtin_fmaf(-q0, s, v[r][e]), rinv, q0));
       t = fminf(fmaxf(t, -127.0f), 127.0f);
       b[e >> 2] |= ((uint32_t)(int)t & 0xffu) << (8 * (e & 3));
     }
     *reinterpret_cast<uint2*>(q + row * K + (int64_t)c * 8) = make_uint2(b[0], b[1]);
   }
+}
+
+// A value that rounds to T exactly as the IEEE quotient x / rs does. For
+// T = bf16, with x and rs bf16 values, that is x * RN(1/rs): the product is
+// within 1.5 fp32 ulps of x / rs, while x / rs (a ratio of two 8-bit
+// significands) is either a bf16 value or at least 2^-17 (relative) away from
+// every bf16 rounding midpoint, far more than the error, so both round to the
+// same bf16 (checked over every pair of bf16 significands, and over the
+// exponent ranges of rows of any scale, by the exhaustive quotient tests).
+// fp16 and fp32 rows keep the division.
+template <int DT>
+__device__ __forceinline__ float div_rs(float x, float rs, float rinv) {
+  if constexpr (DT == SI_DT_BF16) return x * rinv;
+  else return x / rs;
 }
 
 // ---------------------------------------------------------------------------
@@ -170,6 +189,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
     ss = block_sum(ss, lds);
     const float var = round_to(ss * factor, DT);
     const float rs = round_to(sqrtf(round_to(var + eps, DT)), DT);
+    const float rinv = 1.0f / rs;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int c = (int)threadIdx.x + r * 256;
@@ -177,7 +197,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
       float wv[8];
       load8<DT>(w, (int64_t)c * 8, wv);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[r][e] = round_to(round_to(v[r][e] / rs, DT) * wv[e], DT);
+      for (int e = 0; e < 8; ++e) v[r][e] = round_to(round_to(div_rs<DT>(v[r][e], rs, rinv), DT) * wv[e], DT);
       if (y != nullptr) store8<DT>(y, m * K + (int64_t)c * 8, v[r]);
     }
     if (q != nullptr) quant_row<R>(v, nch, m, K, q, scale, lds);
