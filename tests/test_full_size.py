@@ -17,6 +17,10 @@
   layer (packed_kv_cache.py:753-854), from a previous cache packed with the
   same plan and with a different one: buckets, scales and stats bit-exact to
   the oracle.
+* evict of 25% of the token-heads of that layer (packed_kv_cache.py:666-751),
+  given as the reference's set of (t, h) pairs: the removed count, the
+  compacted buckets and scales, the byte count and the unpacked K/V bit-exact
+  to the oracle.
 """
 
 import numpy as np
@@ -141,3 +145,26 @@ def test_config3_reuse_50_percent_7b_layer(dev, same_plan):
     if not same_plan:
         assert abs(stats["skipped_precision"] / (S * H) - 0.5 * 0.625) < 0.01
     assert_cache_equal(cur, ref)
+
+
+@pytest.mark.gpu
+def test_config3_evict_25_percent_7b_layer(dev):
+    from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan
+    B, H, S, D = 1, 32, 8192, 128
+    k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=51, outlier_frac=0.01)
+    codes = mixed_codes(S, H, seed=52, probs=MIX)
+    rng = np.random.default_rng(53)
+    flat = rng.choice(S * H, S * H // 4, replace=False)
+    victims = {(int(e // H), int(e % H)) for e in flat}
+    print(f"config-3 evict: S={S} H={H} D={D} victims={len(victims)}", flush=True)
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    cache = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    removed = cache.evict(victims)
+    ref = oracle_pack(k, v, codes)
+    assert removed == O.kv_evict(ref, victims) == len(victims)
+    assert_cache_equal(cache, ref)  # buckets, scales, indices and memory_bytes
+    k_out, v_out = cache.unpack()
+    rk, rv = O.kv_unpack(ref)
+    np.testing.assert_array_equal(to_np(k_out), rk)
+    np.testing.assert_array_equal(to_np(v_out), rv)
+    assert cache.evict(victims) == 0  # already absent: not counted again
