@@ -210,6 +210,192 @@ __device__ __forceinline__ bool h_exact(uint32_t bits, float s) {
 }
 
 // ---------------------------------------------------------------------------
+// The three parts of one 64-key tile for the 32 queries of a wave.
+//
+// tile_qk: S^T = K Q^T - m on v_mfma_f32_32x32x16_f16. The accumulators start
+// at -m_run (0 before the first tile), so the MFMAs return the scores already
+// shifted by the running max; lane l holds scores of query l % 32 for 16 keys
+// (lane l ^ 32 the other 16). K fragments of k-step ks+1 are read while the
+// MFMAs of k-step ks run. Raises the wave priority (the caller lowers it after
+// the tile's last P.V MFMA): when both waves of a SIMD have instructions
+// ready, the one feeding the matrix core issues first.
+template <int D>
+__device__ __forceinline__ void tile_qk(const _Float16 (*Ks)[D + KPAD], const v8h* qf, int col,
+                                        int grp, float m_run, v16f (&sacc)[2]) {
+  constexpr int KS = D / 16;
+  const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[kb][r] = c0;
+  v8h ka[2][2];
+  auto load_k = [&](int ks, v8h* a) __attribute__((always_inline)) {
+    a[0] = *reinterpret_cast<const v8h*>(&Ks[col][ks * 16 + 8 * grp]);
+    a[1] = *reinterpret_cast<const v8h*>(&Ks[32 + col][ks * 16 + 8 * grp]);
+  };
+  load_k(0, ka[0]);
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + 1 < KS) load_k(ks + 1, ka[(ks + 1) & 1]);
+    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][0], qf[ks], sacc[0], 0, 0, 0);
+    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][1], qf[ks], sacc[1], 0, 0, 0);
+    if (ks + 1 < KS) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two reads of ks+1
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // then the two MFMAs of ks
+    }
+  }
+}
+
+// tile_softmax: online softmax of one tile's shifted scores in the log2 domain
+// (Q carries sm_scale * log2(e)). Keys at or past nv are masked. The running
+// max is raised only when a score exceeds it by more than 8 (a factor 2^8),
+// and always at the first tile, so the output rescale is rare. P = 2^(s - m)
+// as fp16 pairs (the B operand of the P.V MFMAs); the row sum adds the same
+// fp16 values in fp32 (v_dot2_f32_f16 with {1, 1}).
+template <int D>
+__device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, float& m_run,
+                                             float& l_run, v16f* o, uint32_t (&pw)[16]) {
+  constexpr int DB = D / 32;
+  const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
+  if (nv < BN) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (kb * 32 + 8 * (r >> 2) + 4 * grp + (r & 3) >= nv) sacc[kb][r] = -INFINITY;
+  }
+  float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], sacc[kb][r]);
+  float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const bool raise = m_run == -INFINITY || tmax > 8.0f;
+  if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+    const float m_new = raise ? tmax - c0 : m_run;
+    const float alpha = exp2f(m_run - m_new);
+    const float delta = m_new + c0;  // tmax when raised, else 0
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kb][r] -= delta;
+    m_run = m_new;
+  }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // v_exp_f32: arguments are <= 8 here; results below 2^-126 flush to 0
+      const h2 pp = {(_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j]),
+                     (_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j + 1])};
+      pw[8 * kb + j] = as_u32(pp);
+    }
+  float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int w = 0; w < 16; ++w) ps[w & 3] = __builtin_amdgcn_fdot2(as_h2(pw[w]), ones, ps[w & 3], false);
+  const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  l_run += psum + __shfl_xor(psum, 32, 64);
+}
+
+// tile_pv: O^T += V^T P^T over four 16-key chunks. The score registers are
+// the B operand: the k order of an MFMA only has to agree between A and B, so
+// V^T is read in the score accumulator's key order 8*(i/4) + 4*(l/32) + i%4.
+// V^T fragments stream two (chunk, row block) steps ahead of their MFMA.
+template <int D>
+__device__ __forceinline__ void tile_pv(const _Float16 (*Vt)[AttnCfg<D>::VPITCH],
+                                        const uint32_t (&pw)[16], int col, int grp, v16f* o) {
+  constexpr int DB = D / 32;
+  auto load_v = [&](int i) __attribute__((always_inline)) {
+    const int c = i / DB, db = i % DB;
+    const _Float16* vrow = &Vt[db * 32 + col][c * 16 + 4 * grp];
+    const v4h lo = *reinterpret_cast<const v4h*>(vrow);
+    const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
+    return v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  constexpr int NV = 4 * DB;
+  v8h va[3];
+  va[0] = load_v(0);
+  va[1] = load_v(1);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (i + 2 < NV) va[(i + 2) % 3] = load_v(i + 2);
+    const int c = i / DB, db = i % DB;
+    const int base = 4 * c;  // keys 16c .. 16c+15 of the lane's score order
+    const v4i pi = {(int)pw[base], (int)pw[base + 1], (int)pw[base + 2], (int)pw[base + 3]};
+    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[i % 3], __builtin_bit_cast(v8h, pi), o[db], 0, 0, 0);
+  }
+}
+
+// Q^T fragments (B operand of S^T = K Q^T) of query m: dims ks*16 + 8*grp + 0..7,
+// times sm_scale * log2(e), in fp16 (zeros past the last query).
+template <int D, int QDT>
+__device__ __forceinline__ void load_q(const uint16_t* __restrict__ Q, int64_t b, int64_t H,
+                                       int64_t h, int64_t Sq, int64_t m, int grp,
+                                       float scale_log2, v8h* qf) {
+  const bool m_ok = m < Sq;
+  const uint16_t* qrow = Q + (((b * H + h) * Sq) + (m_ok ? m : 0)) * D;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (m_ok) raw = *reinterpret_cast<const uint4*>(qrow + ks * 16 + 8 * grp);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qf[ks][2 * i] = (_Float16)(q_to_f<QDT>(w[i] & 0xffffu) * scale_log2);
+      qf[ks][2 * i + 1] = (_Float16)(q_to_f<QDT>(w[i] >> 16) * scale_log2);
+    }
+  }
+}
+
+// Evicted / absent keys (score 0, value 0) join the softmax denominator
+// (n_ev * 2^(0 - m)); then row m of O^T, divided by the row sum, is stored
+// at out + obase in out_dtype.
+template <int D>
+__device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, int n_ev,
+                                            bool m_ok, int64_t obase, int grp, void* O, int odt) {
+  constexpr int DB = D / 32;
+  if (n_ev > 0) {
+    const float m_fin = fmaxf(m_run, 0.0f);
+    const float alpha = exp2f(m_run - m_fin);
+    l_run = l_run * alpha + (float)n_ev * exp2f(-m_fin);
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+  }
+  if (!m_ok) return;
+  const float inv = 1.0f / l_run;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = db * 32 + 8 * i + 4 * grp;
+      const float r0 = o[db][4 * i + 0] * inv, r1 = o[db][4 * i + 1] * inv;
+      const float r2 = o[db][4 * i + 2] * inv, r3 = o[db][4 * i + 3] * inv;
+      if (odt == SI_DT_F32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(O) + obase + d) =
+            make_float4(r0, r1, r2, r3);
+      } else {
+        const bool bf = odt == SI_DT_BF16;
+        const uint32_t w0 = (bf ? f32_to_bf16_bits(r0) : f32_to_f16_bits(r0)) |
+                            ((bf ? f32_to_bf16_bits(r1) : f32_to_f16_bits(r1)) << 16);
+        const uint32_t w1 = (bf ? f32_to_bf16_bits(r2) : f32_to_f16_bits(r2)) |
+                            ((bf ? f32_to_bf16_bits(r3) : f32_to_f16_bits(r3)) << 16);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(O) + obase + d) = make_uint2(w0, w1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused dequantize + bidirectional attention over a packed KV cache.
 //
 // out = softmax(q k^T * sm_scale) v with no mask, k/v being the values
@@ -270,20 +456,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 
   // Q^T fragments (B operand of S^T = K Q^T): query m, dims ks*16 + 8*grp + 0..7.
   v8h qf[KS];
-  {
-    const uint16_t* qrow = Q + (((b * H + h) * Sq) + (m_ok ? m : 0)) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (m_ok) raw = *reinterpret_cast<const uint4*>(qrow + ks * 16 + 8 * grp);
-      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qf[ks][2 * i] = (_Float16)(q_to_f<QDT>(w[i] & 0xffffu) * scale_log2);
-        qf[ks][2 * i + 1] = (_Float16)(q_to_f<QDT>(w[i] >> 16) * scale_log2);
-      }
-    }
-  }
+  load_q<D, QDT>(Q, b, H, h, Sq, m, grp, scale_log2, qf);
 
   // Tile schedule: the head's list regions in order fp32, fp16, int8, int4.
   const int32_t* cnt = counts + h * 8;
@@ -523,119 +696,14 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     }
   };
 
-  // S^T = K Q^T, online softmax and O^T += V^T P^T for tile tt in buffer buf.
-  auto compute_tile = [&](auto PC, int tt, int buf) __attribute__((always_inline)) {
-    constexpr int P = decltype(PC)::value;
-    const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
-    // ---- S^T = K Q^T - m for the tile's 64 keys ----
-    // The accumulators start at -m_run (0 before the first tile), so the MFMAs
-    // return the scores already shifted by the running max.
-    // K fragments of k-step ks+1 are read while the MFMAs of k-step ks run.
-    const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
+  // S^T = K Q^T, online softmax and O^T += V^T P^T for the tile in buffer buf.
+  auto compute_tile = [&](int nv, int buf) __attribute__((always_inline)) {
     v16f sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = c0;
-    {
-      v8h ka[2][2];
-      auto load_k = [&](int ks, v8h* a) __attribute__((always_inline)) {
-        a[0] = *reinterpret_cast<const v8h*>(&Ks[buf][col][ks * 16 + 8 * grp]);
-        a[1] = *reinterpret_cast<const v8h*>(&Ks[buf][32 + col][ks * 16 + 8 * grp]);
-      };
-      load_k(0, ka[0]);
-      // Raised wave priority from the first QK^T MFMA to the last P.V MFMA: when
-      // both waves of a SIMD have instructions ready, the one feeding the
-      // matrix core issues first (S=8192: 1.42 -> 1.38 ms).
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) load_k(ks + 1, ka[(ks + 1) & 1]);
-        sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][0], qf[ks], sacc[0], 0, 0, 0);
-        sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][1], qf[ks], sacc[1], 0, 0, 0);
-        if (ks + 1 < KS) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two reads of ks+1
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // then the two MFMAs of ks
-        }
-      }
-    }
-
-    // ---- online softmax (log2 domain; Q carries sm_scale * log2(e)) ----
-    if (nv < BN) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kb * 32 + 8 * (r >> 2) + 4 * grp + (r & 3) >= nv) sacc[kb][r] = -INFINITY;
-    }
-    float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], sacc[kb][r]);
-    // Shifted tile max; the running max is raised only when a score exceeds it
-    // by more than 8 (a factor 2^8), and always at the first tile.
-    float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const bool raise = m_run == -INFINITY || tmax > 8.0f;
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-      const float m_new = raise ? tmax - c0 : m_run;
-      const float alpha = exp2f(m_run - m_new);
-      const float delta = m_new + c0;  // tmax when raised, else 0
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb][r] -= delta;
-      m_run = m_new;
-    }
-    // P = 2^(s - m) as fp16 pairs (the B operand of the P.V MFMAs); the row sum
-    // adds the same fp16 values in fp32 (v_dot2_f32_f16 with {1, 1}).
     uint32_t pw[16];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        // v_exp_f32: arguments are <= 8 here; results below 2^-126 flush to 0
-        const h2 pp = {(_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j]),
-                       (_Float16)__builtin_amdgcn_exp2f(sacc[kb][2 * j + 1])};
-        pw[8 * kb + j] = as_u32(pp);
-      }
-    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-    for (int w = 0; w < 16; ++w) ps[w & 3] = __builtin_amdgcn_fdot2(as_h2(pw[w]), ones, ps[w & 3], false);
-    const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
-    l_run += psum + __shfl_xor(psum, 32, 64);
-
-    // ---- O^T += V^T P^T over four 16-key chunks ----
-    {
-      // V^T fragments stream two (chunk, row block) steps ahead of their MFMA.
-      auto load_v = [&](int i) __attribute__((always_inline)) {
-        const int c = i / DB, db = i % DB;
-        const _Float16* vrow = &Vt[buf][db * 32 + col][c * 16 + 4 * grp];
-        const v4h lo = *reinterpret_cast<const v4h*>(vrow);
-        const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
-        return v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      };
-      constexpr int NV = 4 * DB;
-      v8h va[3];
-      va[0] = load_v(0);
-      va[1] = load_v(1);
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        if (i + 2 < NV) va[(i + 2) % 3] = load_v(i + 2);
-        const int c = i / DB, db = i % DB;
-        const int base = 4 * c;  // keys 16c .. 16c+15 of the lane's score order
-        const v4i pi = {(int)pw[base], (int)pw[base + 1], (int)pw[base + 2], (int)pw[base + 3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[i % 3], __builtin_bit_cast(v8h, pi), o[db], 0, 0, 0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    }
+    tile_qk<D>(Ks[buf], qf, col, grp, m_run, sacc);
+    tile_softmax<D>(sacc, nv, grp, m_run, l_run, o, pw);
+    tile_pv<D>(Vt[buf], pw, col, grp, o);
+    __builtin_amdgcn_s_setprio(0);
   };
 
   int buf = 0;
@@ -652,7 +720,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     fetch_slots(t0 + 2);
     lds_barrier();
     for (int tt = t0; tt < t1; ++tt) {
-      compute_tile(PC, tt, buf);
+      compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(tt, P)), buf);
       // Decode the next tile into the other buffer (after the phase's last
       // tile: a clamped copy nobody reads), then prefetch.
       decode_tile(PC, min(tt + 1, t_last), buf ^ 1);
@@ -669,40 +737,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   run_phase(std::integral_constant<int, SI_PREC_INT8>{});
   run_phase(std::integral_constant<int, SI_PREC_INT4>{});
 
-  // Evicted / absent keys: score 0, value 0.
-  if (n_ev > 0) {
-    const float m_fin = fmaxf(m_run, 0.0f);
-    const float alpha = exp2f(m_run - m_fin);
-    l_run = l_run * alpha + (float)n_ev * exp2f(-m_fin);
-#pragma unroll
-    for (int i = 0; i < DB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-  }
-
-  if (!m_ok) return;
-  const float inv = 1.0f / l_run;
-  const int64_t obase = b * os.b + h * os.h + m * os.s;
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = db * 32 + 8 * i + 4 * grp;
-      const float r0 = o[db][4 * i + 0] * inv, r1 = o[db][4 * i + 1] * inv;
-      const float r2 = o[db][4 * i + 2] * inv, r3 = o[db][4 * i + 3] * inv;
-      if (odt == SI_DT_F32) {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(O) + obase + d) =
-            make_float4(r0, r1, r2, r3);
-      } else {
-        const bool bf = odt == SI_DT_BF16;
-        const uint32_t w0 = (bf ? f32_to_bf16_bits(r0) : f32_to_f16_bits(r0)) |
-                            ((bf ? f32_to_bf16_bits(r1) : f32_to_f16_bits(r1)) << 16);
-        const uint32_t w1 = (bf ? f32_to_bf16_bits(r2) : f32_to_f16_bits(r2)) |
-                            ((bf ? f32_to_bf16_bits(r3) : f32_to_f16_bits(r3)) << 16);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(O) + obase + d) = make_uint2(w0, w1);
-      }
-    }
-  }
+  finish_rows<D>(o, m_run, l_run, n_ev, m_ok, b * os.b + h * os.h + m * os.s, grp, O, odt);
 }
 
 template <int D, int QDT, bool O32>
