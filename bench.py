@@ -74,6 +74,26 @@ def make_kv(gen, device, dtype):
     return k.to(dtype), v.to(dtype)
 
 
+RAMP_MS = 60.0
+
+
+def ramp(torch, fn, ms: float = RAMP_MS) -> None:
+    """Run ``fn`` back to back, untimed, for at least ``ms`` milliseconds. The
+    GPU raises its clocks over the first ~30 ms of sustained load after an
+    idle gap (the packed attention at S=8192 runs 1384, 1227, 1186, then
+    1177 us per launch in successive 10-launch windows), so every timed
+    region below starts after such a ramp of its own launches."""
+    t0 = time.perf_counter()
+    batch = 1
+    while True:
+        for _ in range(batch):  # launches queue up back to back between synchronizations
+            fn()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= ms:
+            return
+        batch = min(2 * batch, 64)
+
+
 class EventTimer:
     """HIP events recorded on the stream the kernels are launched on."""
 
@@ -82,6 +102,7 @@ class EventTimer:
 
     def time(self, fn, reps: int) -> float:
         torch = self.torch
+        ramp(torch, fn)
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record(self.stream)
@@ -150,12 +171,15 @@ def bench_kv(torch, dev, steps, warmup):
     # synchronizations, timed by events on the launch stream; an event
     # between the pack and the unpack half of every step gives each kernel's
     # average launch time (32 launches per half, no event between them).
-    for _ in range(max(1, warmup)):
+    def step_cold():
         for L in layers:
             pack(L)
         for L in layers:
             unpack(L)
-    torch.cuda.synchronize()
+
+    for _ in range(max(1, warmup)):
+        step_cold()
+    ramp(torch, step_cold)
     cev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     t0 = time.perf_counter()
     for r in range(steps):
