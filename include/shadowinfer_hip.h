@@ -59,6 +59,14 @@ typedef void* si_stream_t;
 /* Version of this ABI (SI_ABI_VERSION). No reference counterpart. */
 int si_abi_version(void);
 
+/* Self-check, no reference counterpart: converts every one of the 2^32 fp32
+ * bit patterns to bf16 with the conversion the kernels use (gfx950's
+ * v_cvt_pk_bf16_f32, NaN mapped to 0x7FC0) and compares with round-to-nearest-
+ * even bit arithmetic. counts: device uint64[2], zeroed by the caller; adds
+ * the mismatches of the two-value form to counts[0] and of the one-value form
+ * to counts[1] (both stay 0 on a correct device). */
+int si_check_bf16_convert(unsigned long long* counts, si_stream_t stream);
+
 /* Thread-local text of the last failure (empty string if none). Replaces the
  * TORCH_CHECK messages of shadowinfer/kernels/cpp/quantize_int4.cu:176-177. */
 const char* si_last_error(void);
@@ -442,10 +450,24 @@ int si_add_rmsnorm_rows(const void* x, const void* residual, int dtype, int64_t 
  * -> q, k, v [B, H, S, D]; q and k rotated as q * cos + rotate_half(q) * sin
  * in dtype (each product rounded, then the sum) with the rotate-half tables
  * cos_table, sin_table [S, D] (diffusion_llama.py:505-514). D = 64 or 128;
- * all pointers 16-byte aligned. */
+ * all pointers 16-byte aligned. k and v both NULL: only q is written (K and V
+ * then go into the packed cache through si_kv_pack_rope_flat). */
 int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
                   const void* cos_table, const void* sin_table, void* q, void* k, void* v,
                   si_stream_t stream);
+
+/* si_rope_split's K and V rows packed straight into the buckets: the same
+ * bytes as si_rope_split followed by si_kv_pack_flat on its k and v (the
+ * attention layer's pack, pytorch_backend.py:521-548, on the post-RoPE K/V of
+ * diffusion_llama.py:362-373), reading each K/V row from the projection
+ * output qkv [B*S, 3*H*D] (q | k | v column blocks) and rotating K on the way.
+ * dtype bf16 or fp16 (the buckets' scale dtype too); D = 64 or 128; group a
+ * multiple of 8 dividing D with group/8 a power of two; qkv, cos_table and
+ * sin_table 16-byte aligned. flat, counts and buckets as for si_kv_pack_flat. */
+int si_kv_pack_rope_flat(const void* qkv, const void* cos_table, const void* sin_table,
+                         int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t group,
+                         const int8_t* code, const int32_t* slot, const int64_t* const* flat,
+                         const int64_t* counts, void* const* buckets, si_stream_t stream);
 
 /* DiffusionLlamaMLP's silu(gate) * up (shadowinfer/models/diffusion_llama.py:332-333)
  * and the down INT8Linear's activation quantization (int8_linear.py:96-98):

@@ -44,19 +44,32 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0.
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (torch's bf16
+// NaN). gfx950's v_cvt_pk_bf16_f32 rounds to nearest even exactly like the
+// bit arithmetic u + 0x7FFF + ((u >> 16) & 1), >> 16 on every non-NaN fp32
+// pattern (denormals and infinities included; si_check_bf16_convert compares
+// all 2^32 patterns on the device); it keeps a NaN's sign and payload, so NaN
+// is mapped to 0x7FC0 here.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t h = (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
+  return f != f ? 0x7fc0u : h;
+}
+
+// Two values at once, a in the low half (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {a, b};
+  uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2_t));
+  if (a != a) w = (w & 0xffff0000u) | 0x7fc0u;
+  if (b != b) w = (w & 0x0000ffffu) | 0x7fc00000u;
+  return w;
 }
 
 // Same rounding without the NaN test, for values known to be finite.
 __device__ __forceinline__ float round_bf16_finite(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return __uint_as_float(u & 0xffff0000u);
+  const uint32_t h = (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
+  return __uint_as_float(h << 16);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {

@@ -625,42 +625,133 @@ __global__ __launch_bounds__(256) void kv_pack_fast(const void* __restrict__ kin
   }
 }
 
+// K/V rows taken from a q|k|v projection instead of dense [B, H, S, D]
+// tensors: row (b, h, t) of K is qkv[(b*S + t), H*D + h*D .. +D] with RoPE
+// applied, row (b, h, t) of V is qkv[(b*S + t), 2*H*D + h*D .. +D] as it is.
+// cos/sin: [S, D] tables in the K/V dtype.
+struct RopeSrc {
+  const void* qkv;
+  const void* cos;
+  const void* sin;
+  int S;
+  int H;
+};
+
+// RoPE on the EPL values of this lane's chunk of a K row (the reference's
+// q * cos + rotate_half(q) * sin in the row dtype T, each product rounded to
+// T, then the sum; the same arithmetic as rope_split): lanes of the first
+// half of the row take the partner value x[d + D/2] from lane ^ (LPR/2),
+// subtract its product with sin[d]; lanes of the second half add x[d - D/2]
+// times sin[d]. Every lane of the row group must call it (cross-lane reads).
+template <int DT, int LPR>
+__device__ __forceinline__ void rope_chunk(float* x, int64_t t, int lane, const RopeSrc& rs) {
+  static_assert(DT == SI_DT_BF16 || DT == SI_DT_F16, "16-bit rows");
+  constexpr int EPL = Chunk<DT>::EPL;
+  constexpr int D = EPL * LPR;
+  float xp[EPL], c[EPL], sn[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) xp[e] = __shfl_xor(x[e], LPR / 2, 64);
+  // 16-byte loads of the table chunks (reused by every head: plain loads stay in L2)
+  const int64_t el = t * D + lane * EPL;
+  const uint4 cw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(rs.cos) + el);
+  const uint4 sw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(rs.sin) + el);
+  const uint32_t cws[4] = {cw.x, cw.y, cw.z, cw.w}, sws[4] = {sw.x, sw.y, sw.z, sw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[2 * i] = DT == SI_DT_BF16 ? bf16_bits_to_f32(cws[i] & 0xffffu) : f16_bits_to_f32(cws[i] & 0xffffu);
+    c[2 * i + 1] = DT == SI_DT_BF16 ? bf16_bits_to_f32(cws[i] >> 16) : f16_bits_to_f32(cws[i] >> 16);
+    sn[2 * i] = DT == SI_DT_BF16 ? bf16_bits_to_f32(sws[i] & 0xffffu) : f16_bits_to_f32(sws[i] & 0xffffu);
+    sn[2 * i + 1] = DT == SI_DT_BF16 ? bf16_bits_to_f32(sws[i] >> 16) : f16_bits_to_f32(sws[i] >> 16);
+  }
+  const bool first = lane < LPR / 2;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float a = round_to(x[e] * c[e], DT);
+    const float b = round_to(xp[e] * sn[e], DT);
+    x[e] = round_to(first ? a - b : a + b, DT);
+  }
+}
+
 // Pack in bucket order: block x takes RPP*U consecutive rows (entry, b) of
 // one precision's bucket (the flat index lists give each row's dense row
 // b*H*S + h*S + t), so every wave quantizes a single precision and the bucket
 // rows are written contiguously. blk_end[p]: first block after precision p's.
-template <int DT, int LPR, int U, int P, int NT>
+// Element offsets of this lane's K and V chunks of row (bb, flat = h*S + t):
+// dense [B, H, S, D] tensors, or the q|k|v projection rows with ROPE (t is
+// then returned for the cos/sin tables).
+template <bool ROPE, int D, int EPL>
+__device__ __forceinline__ void row_offsets(int64_t bb, int64_t flat, int64_t HS, int lane,
+                                            const RopeSrc& rs, int64_t& koff, int64_t& voff,
+                                            int64_t& t) {
+  if constexpr (ROPE) {
+    const int64_t h = flat / rs.S;
+    t = flat - h * rs.S;
+    koff = ((bb * rs.S + t) * 3 * rs.H + rs.H + h) * D + lane * EPL;
+    voff = koff + (int64_t)rs.H * D;
+  } else {
+    koff = voff = (bb * HS + flat) * D + lane * EPL;
+    t = 0;
+  }
+}
+
+template <int DT, int LPR, int U, int P, int NT, bool ROPE>
 __device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
                                                  const void* __restrict__ vin,
                                                  const UnpackLists& L, int64_t lb, int B,
-                                                 int64_t HS, int lpg, const Buckets& bk) {
+                                                 int64_t HS, int lpg, const Buckets& bk,
+                                                 const RopeSrc& rs) {
   constexpr int EPL = Chunk<DT>::EPL;
   constexpr int D = EPL * LPR;
   constexpr int RPP = NT / LPR;
   const int lane = threadIdx.x % LPR;
   const int64_t rows = L.n[P] * B;
   const int64_t r0 = lb * (RPP * U) + threadIdx.x / LPR;
+  if (ROPE) {
+    kin = rs.qkv;
+    vin = rs.qkv;
+  }
   if constexpr (DT == SI_DT_BF16) {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     uint32_t wk[U][4], wv[U][4];
-    int64_t sl[U], bb[U];
+    int64_t sl[U], bb[U], tk[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t r = r0 + u * RPP;
       sl[u] = -1;
+      tk[u] = 0;
+      if constexpr (ROPE) {  // rows past the end still take part in the lane exchange
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wk[u][i] = wv[u][i] = 0u;
+      }
       if (r < rows) {
         sl[u] = r / B;
         bb[u] = r - sl[u] * B;
-        const int64_t off = ((bb[u] * HS + L.flat[P][sl[u]]) * D + lane * EPL) * 2;
+        int64_t ko, vo;
+        row_offsets<ROPE, D, EPL>(bb[u], L.flat[P][sl[u]], HS, lane, rs, ko, vo, tk[u]);
         const u32x4 a = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + off));
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kin) + ko * 2));
         const u32x4 b = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vin) + off));
+            reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vin) + vo * 2));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           wk[u][i] = a[i];
           wv[u][i] = b[i];
         }
+      }
+    }
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[2 * i] = bf16_bits_to_f32(wk[u][i] & 0xffffu);
+          x[2 * i + 1] = bf16_bits_to_f32(wk[u][i] >> 16);
+        }
+        rope_chunk<DT, LPR>(x, tk[u], lane, rs);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          wk[u][i] = f32x2_to_bf16x2_bits(x[2 * i], x[2 * i + 1]);
       }
     }
 #pragma unroll
@@ -670,18 +761,28 @@ __device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
                                   nullptr, nullptr);
   } else {
     float xk[U][EPL], xv[U][EPL];
-    int64_t sl[U], bb[U];
+    int64_t sl[U], bb[U], tk[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t r = r0 + u * RPP;
       sl[u] = -1;
+      tk[u] = 0;
+      if constexpr (ROPE) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) xk[u][e] = xv[u][e] = 0.0f;
+      }
       if (r < rows) {
         sl[u] = r / B;
         bb[u] = r - sl[u] * B;
-        const int64_t el = (bb[u] * HS + L.flat[P][sl[u]]) * D + lane * EPL;
-        load_chunk<DT>(kin, el, xk[u]);
-        load_chunk<DT>(vin, el, xv[u]);
+        int64_t ko, vo;
+        row_offsets<ROPE, D, EPL>(bb[u], L.flat[P][sl[u]], HS, lane, rs, ko, vo, tk[u]);
+        load_chunk<DT>(kin, ko, xk[u]);
+        load_chunk<DT>(vin, vo, xv[u]);
       }
+    }
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) rope_chunk<DT, LPR>(xk[u], tk[u], lane, rs);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -691,20 +792,24 @@ __device__ __forceinline__ void pack_bucket_rows(const void* __restrict__ kin,
   }
 }
 
-template <int DT, int LPR, int U, int NT>
+template <int DT, int LPR, int U, int NT, bool ROPE = false>
 __global__ __launch_bounds__(NT) void kv_pack_lists(const void* __restrict__ kin,
                                                      const void* __restrict__ vin, UnpackLists L,
-                                                     int B, int H, int S, int lpg, Buckets bk) {
+                                                     int B, int H, int S, int lpg, Buckets bk,
+                                                     RopeSrc rs = RopeSrc{}) {
   const int64_t blk = blockIdx.x;
   const int64_t HS = (int64_t)H * S;
   if (blk < L.blk_end[0]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_FP32, NT>(kin, vin, L, blk, B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP32, NT, ROPE>(kin, vin, L, blk, B, HS, lpg, bk, rs);
   } else if (blk < L.blk_end[1]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_FP16, NT>(kin, vin, L, blk - L.blk_end[0], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_FP16, NT, ROPE>(kin, vin, L, blk - L.blk_end[0], B, HS,
+                                                         lpg, bk, rs);
   } else if (blk < L.blk_end[2]) {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_INT8, NT>(kin, vin, L, blk - L.blk_end[1], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT8, NT, ROPE>(kin, vin, L, blk - L.blk_end[1], B, HS,
+                                                         lpg, bk, rs);
   } else {
-    pack_bucket_rows<DT, LPR, U, SI_PREC_INT4, NT>(kin, vin, L, blk - L.blk_end[2], B, HS, lpg, bk);
+    pack_bucket_rows<DT, LPR, U, SI_PREC_INT4, NT, ROPE>(kin, vin, L, blk - L.blk_end[2], B, HS,
+                                                         lpg, bk, rs);
   }
 }
 
@@ -2016,4 +2121,67 @@ extern "C" int si_kv_pack_flat(const void* k, const void* v, int dtype, int64_t 
 #undef SI_PL_DT
 #undef SI_PL
   return check_launch("si_kv_pack_flat");
+}
+
+extern "C" int si_kv_pack_rope_flat(const void* qkv, const void* cos, const void* sin, int dtype,
+                                    int64_t B, int64_t H, int64_t S, int64_t D, int64_t group,
+                                    const int8_t* code, const int32_t* slot,
+                                    const int64_t* const* flat, const int64_t* counts,
+                                    void* const* buckets, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype == SI_DT_BF16 || dtype == SI_DT_F16,
+               "si_kv_pack_rope_flat: dtype must be bf16 or fp16 (got %d)", dtype);
+  SI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && (D == 64 || D == 128),
+               "si_kv_pack_rope_flat: bad shape (D must be 64 or 128)");
+  SI_CHECK_ARG(group > 0 && D % group == 0 && group % 8 == 0 && pow2(group / 8),
+               "si_kv_pack_rope_flat: group must divide D and be 8 times a power of two");
+  SI_CHECK_ARG(buckets != nullptr && flat != nullptr && counts != nullptr,
+               "si_kv_pack_rope_flat: NULL table");
+  SI_CHECK_ARG(B * H * S < ((int64_t)1 << 31) && S < ((int64_t)1 << 31),
+               "si_kv_pack_rope_flat: too many rows");
+  if (B * H * S == 0) return SI_OK;
+  SI_CHECK_ARG(qkv != nullptr && cos != nullptr && sin != nullptr,
+               "si_kv_pack_rope_flat: NULL argument");
+  SI_CHECK_ARG(((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(cos) |
+                 reinterpret_cast<uintptr_t>(sin)) & 15) == 0,
+               "si_kv_pack_rope_flat: qkv, cos and sin must be 16-byte aligned");
+  int64_t nsum = 0;
+  for (int p = 0; p < 5; ++p) {
+    SI_CHECK_ARG(counts[p] >= 0, "si_kv_pack_rope_flat: negative count");
+    nsum += counts[p];
+  }
+  SI_CHECK_ARG(nsum == H * S, "si_kv_pack_rope_flat: counts sum to %lld, not S*H = %lld",
+               (long long)nsum, (long long)(H * S));
+  for (int p = 0; p < 4; ++p)
+    SI_CHECK_ARG(counts[p] == 0 || flat[p] != nullptr, "si_kv_pack_rope_flat: NULL flat list %d",
+                 p);
+  const Buckets bk = to_buckets(buckets);
+  hipStream_t st = as_stream(stream);
+  constexpr int U = SI_PACK_LISTS_U;
+  constexpr int NT = SI_PACK_LISTS_NT;
+  const int64_t lpr = D / 8;
+  const int64_t lpg = group / 8;
+  const int64_t rpb = (NT / lpr) * U;
+  UnpackLists L;
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    L.flat[p] = flat[p];
+    L.n[p] = counts[p];
+    acc += ceil_div(counts[p] * B, rpb);
+    L.blk_end[p] = acc;
+  }
+  L.blk_end[4] = acc;
+  if (acc == 0) return SI_OK;
+  const dim3 grid((unsigned)acc);
+  const RopeSrc rs{qkv, cos, sin, (int)S, (int)H};
+#define SI_PR(DT_, L_)                                                                   \
+  kv_pack_lists<DT_, L_, U, NT, true><<<grid, NT, 0, st>>>(nullptr, nullptr, L, (int)B, (int)H, \
+                                                          (int)S, (int)lpg, bk, rs)
+  if (dtype == SI_DT_F16) {
+    if (lpr == 8) SI_PR(SI_DT_F16, 8); else SI_PR(SI_DT_F16, 16);
+  } else {
+    if (lpr == 8) SI_PR(SI_DT_BF16, 8); else SI_PR(SI_DT_BF16, 16);
+  }
+#undef SI_PR
+  return check_launch("si_kv_pack_rope_flat");
 }

@@ -214,7 +214,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const void* __restrict__ x,
 //   out[d+D/2]   = T(T(x[d+D/2] cos[s,d+D/2]) + T(x[d] sin[s,d+D/2]))   (d < D/2)
 // with the cos/sin tables [S, D] in T (the reference's emb = cat(freqs, freqs)
 // cast to the parameter dtype).
-// A thread owns 8 dims of the first half and their 8 partners.
+// A thread owns 8 dims of the first half and their 8 partners. With ko and vo
+// NULL only q is written (K and V then go straight into a packed cache).
 // ---------------------------------------------------------------------------
 template <int DT, int D>
 __global__ __launch_bounds__(256) void rope_split(const void* __restrict__ qkv,
@@ -241,8 +242,10 @@ __global__ __launch_bounds__(256) void rope_split(const void* __restrict__ qkv,
     load8<DT>(cosb, s * D + d + HALF, c1);
     load8<DT>(sinb, s * D + d, s0);
     load8<DT>(sinb, s * D + d + HALF, s1);
+    const int parts = ko != nullptr ? 2 : 1;
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
+      if (part >= parts) break;
       float x0[8], x1[8], y0[8], y1[8];
       load8<DT>(qkv, in + part * H * D, x0);
       load8<DT>(qkv, in + part * H * D + HALF, x1);
@@ -255,6 +258,7 @@ __global__ __launch_bounds__(256) void rope_split(const void* __restrict__ qkv,
       store8<DT>(dst, out, y0);
       store8<DT>(dst, out + HALF, y1);
     }
+    if (vo == nullptr) continue;
     float v0[8], v1[8];
     load8<DT>(qkv, in + 2 * H * D, v0);
     load8<DT>(qkv, in + 2 * H * D + HALF, v1);
@@ -597,9 +601,10 @@ extern "C" int si_rope_split(const void* qkv, int dtype, int64_t B, int64_t S, i
                (long long)D);
   SI_CHECK_ARG(B >= 0 && S >= 0 && H >= 0, "si_rope_split: bad shape");
   if (B * S * H == 0) return SI_OK;
-  SI_CHECK_ARG(qkv && cos_table && sin_table && q && k && v, "si_rope_split: NULL argument");
+  SI_CHECK_ARG(qkv && cos_table && sin_table && q && (k != nullptr) == (v != nullptr),
+               "si_rope_split: NULL argument (k and v are both given or both NULL)");
   SI_CHECK_ARG(aligned16(qkv) && aligned16(cos_table) && aligned16(sin_table) && aligned16(q) &&
-                   aligned16(k) && aligned16(v),
+                   (k == nullptr || (aligned16(k) && aligned16(v))),
                "si_rope_split: pointers must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
   if (dtype == SI_DT_BF16) launch_rope<SI_DT_BF16>(qkv, cos_table, sin_table, B, S, H, D, q, k, v, st);

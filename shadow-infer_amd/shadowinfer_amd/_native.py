@@ -41,12 +41,15 @@ _PTR4 = ctypes.c_void_p * 4
 _SIGNATURES = {
     "si_abi_version": (_i32, []),
     "si_last_error": (ctypes.c_char_p, []),
+    "si_check_bf16_convert": (_i32, [_vp, _vp]),
     "si_plan_workspace_bytes": (_sz, [_i64]),
     "si_plan_scan": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "si_plan_scatter": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "si_kv_pack": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "si_kv_pack_flat": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                _vp, _vp]),
+    "si_kv_pack_rope_flat": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp,
+                                    _vp, _vp, _vp, _vp, _vp]),
     "si_kv_pack_copy": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp]),
     "si_page_write": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _vp,

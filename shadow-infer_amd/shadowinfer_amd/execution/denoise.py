@@ -22,8 +22,9 @@ composes them the way its parts are defined:
   full sequence.
 
 Per computed layer the kernels are: RMSNorm (HIP) -> q|k|v projection (one
-bf16 library GEMM) -> RoPE + head split (HIP) -> KV pack (HIP) -> packed
-attention writing token-major output (HIP) -> o projection (bf16 library
+bf16 library GEMM) -> RoPE of q (HIP) -> KV pack reading K and V straight
+from the projection, K rotated on the way (HIP; the dense K/V are not
+written) -> packed attention writing token-major output (HIP) -> o projection (bf16 library
 GEMM) -> residual add fused with the RMSNorm and the activation quantization
 (HIP) -> gate|up INT8 GEMM (HIP, one GEMM over both weights) ->
 SwiGLU fused with the down projection's activation quantization (HIP) ->
@@ -159,9 +160,15 @@ class PackedDiffusionLlama:
         x = hidden.reshape(T, Hd)
         xn, _, _, _ = row_ops.rmsnorm(x, L.ln1, c.rms_norm_eps)
         qkv = F.linear(xn, L.w_qkv)
-        q, k, v = row_ops.rope_split(qkv, cos, sin, B, S, H, D)
-        cache = PackedKVCache.pack(k, v, None, group_size=c.int4_group_size,
-                                   plan=plan)["packed_kv"]
+        if trace is None and row_ops.rope_pack_supported(qkv.dtype, D, c.int4_group_size):
+            # K and V go from the projection straight into the packed cache
+            q, k, v = row_ops.rope_split(qkv, cos, sin, B, S, H, D, kv=False)
+            cache = PackedKVCache.pack_projection(qkv, cos, sin, B, S, H, D,
+                                                  c.int4_group_size, plan)
+        else:
+            q, k, v = row_ops.rope_split(qkv, cos, sin, B, S, H, D)
+            cache = PackedKVCache.pack(k, v, None, group_size=c.int4_group_size,
+                                       plan=plan)["packed_kv"]
         attn = packed_attention(q, cache, out_dtype=self.dtype, token_major=True)
         o = F.linear(attn.view(T, Hd), L.w_o)
         y2, qx, sx, x1 = row_ops.rmsnorm(x, L.ln2, c.rms_norm_eps, want_y=trace is not None,

@@ -53,24 +53,39 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, want_y: bool = Tr
             (None if xo is None else xo.view(x.shape)))
 
 
-def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, batch: int, seq: int,
-               heads: int, head_dim: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """``qkv [B*S, 3*H*D]`` -> rotated q, rotated k and v, each ``[B, H, S, D]``
-    (models/diffusion_llama.py:362-373); ``cos``/``sin`` ``[S, D]`` in qkv's dtype."""
-    _native.require_device(qkv, "rope_split")
+def _check_rope_args(qkv, cos, sin, batch, seq, heads, head_dim, what):
+    _native.require_device(qkv, what)
     if qkv.shape != (batch * seq, 3 * heads * head_dim):
         raise ValueError(f"qkv must be [{batch * seq}, {3 * heads * head_dim}], got {tuple(qkv.shape)}")
     if cos.shape != (seq, head_dim) or sin.shape != (seq, head_dim):
         raise ValueError(f"cos/sin must be [{seq}, {head_dim}]")
     if cos.dtype != qkv.dtype or sin.dtype != qkv.dtype:
         raise ValueError("cos/sin must have qkv's dtype")
+
+
+def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, batch: int, seq: int,
+               heads: int, head_dim: int, kv: bool = True
+               ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """``qkv [B*S, 3*H*D]`` -> rotated q, rotated k and v, each ``[B, H, S, D]``
+    (models/diffusion_llama.py:362-373); ``cos``/``sin`` ``[S, D]`` in qkv's dtype.
+    ``kv=False`` writes q only (k and v are returned as None)."""
+    _check_rope_args(qkv, cos, sin, batch, seq, heads, head_dim, "rope_split")
     src = qkv.contiguous()
-    q, k, v = (torch.empty(batch, heads, seq, head_dim, dtype=qkv.dtype, device=qkv.device)
-               for _ in range(3))
+    q = torch.empty(batch, heads, seq, head_dim, dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty_like(q) if kv else None
+    v = torch.empty_like(q) if kv else None
     _native.call("si_rope_split", src.data_ptr(), _native.dtype_code(qkv.dtype), batch, seq,
                  heads, head_dim, cos.contiguous().data_ptr(), sin.contiguous().data_ptr(),
-                 q.data_ptr(), k.data_ptr(), v.data_ptr(), _native.stream(qkv.device))
+                 q.data_ptr(), _native.ptr(k), _native.ptr(v), _native.stream(qkv.device))
     return q, k, v
+
+
+def rope_pack_supported(dtype: torch.dtype, head_dim: int, group_size: int) -> bool:
+    """Whether ``PackedKVCache.pack_projection`` (si_kv_pack_rope_flat) takes
+    these shapes: bf16/fp16 rows, D = 64 or 128, int4 groups of 8 * 2^k dividing D."""
+    g = group_size if head_dim % group_size == 0 else head_dim
+    return (dtype in (torch.bfloat16, torch.float16) and head_dim in (64, 128)
+            and g % 8 == 0 and (g // 8) & (g // 8 - 1) == 0)
 
 
 def swiglu_quant(gate_up: torch.Tensor, want_h: bool = False

@@ -67,6 +67,45 @@ class PackedKVCache:
         return {"packed_kv": cache, "memory_bytes": cache.memory_bytes(),
                 "memory_mb": cache.memory_mb()}
 
+    @classmethod
+    def pack_projection(cls, qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                        batch_size: int, seq_len: int, num_heads: int, head_dim: int,
+                        group_size: int, plan: Any) -> "PackedKVCache":
+        """The cache ``pack(k, v, None, group_size, plan)`` returns for the
+        post-RoPE K and V of an attention layer (models/diffusion_llama.py:362-373),
+        read straight from the q|k|v projection ``qkv [B*S, 3*H*D]`` with the
+        rotate-half tables ``cos``/``sin`` ``[S, D]`` (si_kv_pack_rope_flat): the
+        dense K/V are never written. bf16/fp16, D = 64 or 128."""
+        B, S, H, D = batch_size, seq_len, num_heads, head_dim
+        if qkv.shape != (B * S, 3 * H * D):
+            raise ValueError(f"qkv must be [{B * S}, {3 * H * D}], got {tuple(qkv.shape)}")
+        if plan.seq_len != S or plan.num_heads != H:
+            raise ValueError(
+                "PrecisionPlan shape mismatch: plan "
+                f"(seq_len={plan.seq_len}, num_heads={plan.num_heads}) vs "
+                f"tensor (seq_len={S}, num_heads={H})")
+        _native.require_device(qkv, "PackedKVCache.pack_projection")
+        dev = qkv.device
+        cache = cls(B, H, S, D, device=dev)
+        grouping = plan.device_grouping()
+        if grouping.code.device != dev:
+            grouping = DeviceGrouping(grouping.code.to(dev), grouping.slot.to(dev),
+                                      list(grouping.counts))
+        g = group_size if D % group_size == 0 else D
+        cache._grouping = grouping
+        cache._group_size = g
+        cache._scale_dtype = qkv.dtype
+        cache._buckets = cache._alloc_buckets(grouping.counts, dev, qkv.dtype)
+        cache._view = None
+        flat = grouping.flat_lists(S, H)
+        counts = (ctypes.c_int64 * 5)(*[int(c) for c in grouping.counts])
+        _native.call("si_kv_pack_rope_flat", qkv.contiguous().data_ptr(),
+                     cos.contiguous().data_ptr(), sin.contiguous().data_ptr(),
+                     _native.dtype_code(qkv.dtype), B, H, S, D, g, grouping.code.data_ptr(),
+                     grouping.slot.data_ptr(), _native.table4([f.data_ptr() for f in flat]),
+                     counts, cache._bucket_table(), _native.stream(dev))
+        return cache
+
     def _do_pack(self, k_tensor: torch.Tensor, v_tensor: torch.Tensor,
                  precision_map: Optional[Dict[int, Dict[int, str]]], group_size: int = 16,
                  plan: Any = None, precomputed: Optional[Dict[str, Any]] = None,

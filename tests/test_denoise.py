@@ -659,3 +659,56 @@ def test_shape_validation_without_gpu():
     with pytest.raises(ValueError):
         DiffusionLlamaShape(mask_token_id=32000)
     assert DiffusionLlamaShape().head_dim == 128
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,S,H,D,group", [(1, 96, 4, 128, 16), (2, 67, 3, 64, 16),
+                                           (1, 300, 2, 128, 32), (2, 33, 5, 64, 8),
+                                           (1, 1, 1, 128, 16)])
+def test_pack_projection_equals_rope_then_pack(dev, dtype, B, S, H, D, group):
+    """PackedKVCache.pack_projection (K and V read from the q|k|v projection,
+    K rotated in the pack kernel) writes the buckets and scales that
+    rope_split followed by PackedKVCache.pack writes, bit for bit, for every
+    precision including fp32 entries and evictions; rope_split with kv=False
+    writes the same q."""
+    from shadowinfer_amd.execution import row_ops
+    from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan
+    from helpers import mixed_codes
+    g = torch.Generator().manual_seed(S * H + D)
+    qkv = (torch.randn(B * S, 3 * H * D, generator=g) * 2).to(dtype).to(dev)
+    qkv[:, H * D: H * D + D] *= 40  # large K rows of head 0: scales far from 1
+    ang = torch.randn(S, D, generator=g) * 3
+    cos, sin = ang.cos().to(dtype).to(dev), ang.sin().to(dtype).to(dev)
+    codes = mixed_codes(S, H, seed=S + D, probs=(1, 1, 2, 2), sink=min(4, S), evicted=0.1)
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    assert row_ops.rope_pack_supported(dtype, D, group)
+    q_ref, k, v = row_ops.rope_split(qkv, cos, sin, B, S, H, D)
+    ref = PackedKVCache.pack(k, v, None, group_size=group, plan=plan)["packed_kv"]
+    q, none_k, none_v = row_ops.rope_split(qkv, cos, sin, B, S, H, D, kv=False)
+    assert none_k is None and none_v is None and torch.equal(q, q_ref)
+    got = PackedKVCache.pack_projection(qkv, cos, sin, B, S, H, D, group, plan)
+    assert got.memory_bytes() == ref.memory_bytes()
+    rb, gb = ref._buckets, got._buckets
+    assert rb.keys() == gb.keys()
+    for name in rb:
+        for part in ("k", "v", "scale_k", "scale_v"):
+            if rb[name][part] is None:
+                assert gb[name][part] is None
+            else:
+                assert torch.equal(gb[name][part].view(torch.uint8),
+                                   rb[name][part].view(torch.uint8)), (name, part)
+    uk, uv = got.unpack()
+    rk, rv = ref.unpack()
+    assert torch.equal(uk, rk) and torch.equal(uv, rv)
+
+
+def test_rope_pack_support_rule():
+    from shadowinfer_amd.execution import row_ops
+    assert row_ops.rope_pack_supported(torch.bfloat16, 128, 16)
+    assert row_ops.rope_pack_supported(torch.float16, 64, 8)
+    assert row_ops.rope_pack_supported(torch.bfloat16, 128, 12)  # 12 does not divide 128: one group of D
+    assert not row_ops.rope_pack_supported(torch.float32, 128, 16)
+    assert not row_ops.rope_pack_supported(torch.bfloat16, 96, 16)
+    assert not row_ops.rope_pack_supported(torch.bfloat16, 128, 4)
+    assert row_ops.rope_pack_supported(torch.bfloat16, 64, 24)  # 24 does not divide 64: one group of D
