@@ -1054,7 +1054,9 @@ enum Kind { K_SCALAR = 0, K_SKINNY = 1, K_TILE_128x128 = 3, K_DMA_256x256 = 6,
             // more blocks than 128x128 when few rows share the weight
             K_DMA_64x64 = 38, K_DMA_64x128 = 39,
             // one block per CU over ceil(N / 256) weight rows (gemm_rows)
-            K_ROWS = 40 };
+            K_ROWS = 40,
+            // four waves over a 128x96 tile (each 32 rows x 96 columns)
+            K_DMA_128x96 = 41 };
 
 struct Plan {
   int kind;
@@ -1144,20 +1146,25 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   } else if (K % 128 == 0) {
     // One tile per CU per wave of tiles. Estimated time = waves of 256 tiles
     // x (tile area / the tile's measured speed relative to 256x256); the
-    // smallest wins. 4096 x 11008: M = 129..256 -> 128x128 (M = 256: 21.7 us),
-    // M = 384..512 -> 256x128, M = 640 -> 128x128, M = 1024 -> 256x192;
-    // 2048 x 22016 x 4096 -> 256x256 (k step 128: 206 -> 199 us against 64);
-    // 2048 x 4096 x 11008 -> 256x128.
-    struct Cand { int kind, bm, bn; double speed; };
-    const Cand cands[4] = {{K_DMA8_256x192_K128, 256, 192, 0.91},
-                           {K_DMA8_256x256_K128, 256, 256, 1.0},
-                           {K_DMA_256x128_K128, 256, 128, 0.81},
-                           {K_DMA8_128x128_24, 128, 128, 0.78}};
+    // smallest wins. 4096 x 11008: M = 129..256 -> 128x96 (230 tiles; M = 256:
+    // 23.8 -> 22.0 us against 128x128), M = 384..512 -> 256x128, M = 640 ->
+    // 128x128, M = 1024 -> 256x192; 2048 x 22016 x 4096 -> 256x256 (k step
+    // 128: 206 -> 199 us against 64); 2048 x 4096 x 11008 -> 256x128. The
+    // 128x96 tile only up to 256 rows and where its grid is one wave filling
+    // at least 192 CUs, as measured (at M = 320 its two waves lose to 256x128,
+    // 37 against 34 us; grids filling fewer CUs belong to the fill model).
+    struct Cand { int kind, bm, bn; double speed; bool one_wave; };
+    const Cand cands[5] = {{K_DMA8_256x192_K128, 256, 192, 0.91, false},
+                           {K_DMA8_256x256_K128, 256, 256, 1.0, false},
+                           {K_DMA_256x128_K128, 256, 128, 0.81, false},
+                           {K_DMA8_128x128_24, 128, 128, 0.78, false},
+                           {K_DMA_128x96, 128, 96, 0.63, true}};
     double best = 0.0;
     int64_t best_tiles = 0;
     kind = K_DMA8_256x192_K128;
     for (const Cand& c : cands) {
       const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+      if (c.one_wave && (tiles > 256 || tiles < 192 || M > 256)) continue;
       const double t = (double)ceil_div(tiles, 256) * c.bm * c.bn / c.speed;
       if (best == 0.0 || t < best * (1.0 - 1e-9)) { best = t; kind = c.kind; best_tiles = tiles; }
     }
@@ -1222,6 +1229,7 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     case K_DMA8_128x128_24: p.bm = 128; p.bn = 128; p.bk = 128; break;
     case K_DMA_64x64: p.bm = 64; p.bn = 64; p.bk = 128; break;
     case K_DMA_64x128: p.bm = 64; p.bn = 128; p.bk = 128; break;
+    case K_DMA_128x96: p.bm = 128; p.bn = 96; p.bk = 128; break;
     default: p.kind = K_TILE_128x128; p.bm = 128; p.bn = 128; p.bk = 128; break;
   }
   if (K % p.bk != 0 && p.bk == 128 && K % 64 == 0 && p.kind != K_TILE_128x128) {
@@ -1283,6 +1291,7 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
     case K_DMA8_128x128_24: SI_DMA(128, 128, 128, 2, 4, 4); break;
     case K_DMA_64x64: SI_DMA(64, 64, 128, 2, 2, 4); break;
     case K_DMA_64x128: SI_DMA(64, 128, 128, 2, 2, 4); break;
+    case K_DMA_128x96: SI_DMA(128, 96, 128, 4, 1, 4); break;
     default: SI_DMA(128, 256, 64, 2, 4, 4); break;
   }
 #undef SI_DMA
