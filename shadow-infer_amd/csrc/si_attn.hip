@@ -13,8 +13,9 @@
 // the tile's keys and lane l ^ 32 the other 16: the online-softmax max and sum
 // need one cross-lane shuffle. O^T = V^T P^T then reuses the score registers
 // as the B operand; the k order of an MFMA only has to match between its A and
-// B operands, so V^T is read from LDS in the key order the score accumulator
-// already has (keys 8*(i/4) + 4*(l/32) + i%4 of each 16-key chunk).
+// B operands, so V^T is read from LDS (V row-major, read with the transposing
+// ds_read_b64_tr_b16) in the key order the score accumulator already has
+// (keys 8*(i/4) + 4*(l/32) + i%4 of each 16-key chunk).
 //
 // Precision: fp16 operands (10-bit mantissa) with fp32 accumulation and an
 // fp32 online softmax; fp16 entries of the cache are exact in fp16, int8/int4
@@ -141,10 +142,15 @@ struct AttnCfg {
   static constexpr int DPT = D / (4 * NW);  // head-dim values per thread in the decode stage
   static constexpr int DGN = 4 * NW;        // dim groups (threads per key group)
   static constexpr int RW = DPT / 2;        // 32-bit words of one key's fp16 values
-  // V^T pitch (fp16) and store rotation that keep the transposed 8-byte stores
-  // at two LDS passes per 32 lanes.
-  static constexpr int VPITCH = 76;
+  // V row pitch (fp16): V is kept row-major like K and read transposed with
+  // ds_read_b64_tr_b16 (tile_pv). A pitch of an odd multiple of 16 dwords puts
+  // the 8-byte reads of the four rows and two 16-dim halves one transposed
+  // read of 32 lanes covers on 64 distinct banks.
+  static constexpr int VROW = D == 128 ? 160 : 96;
 };
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -308,16 +314,24 @@ __device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, f
 // tile_pv: O^T += V^T P^T over four 16-key chunks. The score registers are
 // the B operand: the k order of an MFMA only has to agree between A and B, so
 // V^T is read in the score accumulator's key order 8*(i/4) + 4*(l/32) + i%4.
-// V^T fragments stream two (chunk, row block) steps ahead of their MFMA.
+// V is row-major in LDS; ds_read_b64_tr_b16 transposes 4 keys x 16 dims per
+// 16-lane group: lane r of the group receives M[4j + r/4][r%4] (j = 0..3),
+// where lane i of the group addressed the 4 dims M[i][0..3]. Lane i therefore
+// addresses key k0 + i/4 at dims base + 4*(i%4), and lane r receives dim
+// base + r of keys k0 .. k0+3. V^T fragments stream two (chunk, row block)
+// steps ahead of their MFMA.
 template <int D>
-__device__ __forceinline__ void tile_pv(const _Float16 (*Vt)[AttnCfg<D>::VPITCH],
+__device__ __forceinline__ void tile_pv(const _Float16 (*Vs)[AttnCfg<D>::VROW],
                                         const uint32_t (&pw)[16], int col, int grp, v16f* o) {
   constexpr int DB = D / 32;
+  const int li = col & 15;       // lane within its 16-lane group
+  const int half = col >> 4;     // dims 0..15 or 16..31 of a 32-dim block
   auto load_v = [&](int i) __attribute__((always_inline)) {
     const int c = i / DB, db = i % DB;
-    const _Float16* vrow = &Vt[db * 32 + col][c * 16 + 4 * grp];
-    const v4h lo = *reinterpret_cast<const v4h*>(vrow);
-    const v4h hi = *reinterpret_cast<const v4h*>(vrow + 8);
+    const _Float16* vp = &Vs[c * 16 + 4 * grp + (li >> 2)][db * 32 + 16 * half + 4 * (li & 3)];
+    const v4h lo = __builtin_bit_cast(v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)vp));
+    const v4h hi = __builtin_bit_cast(
+        v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vp + 8 * AttnCfg<D>::VROW)));
     return v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
   constexpr int NV = 4 * DB;
@@ -408,7 +422,7 @@ __device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, i
 // wave owns 32. Tiles follow the head's slot list (one precision per tile).
 // Per tile:
 //  * decode (512 threads, 4 keys x D/32 dims each) from registers loaded one
-//    tile ahead (slot lists two tiles ahead), K row-major and V transposed;
+//    tile ahead (slot lists two tiles ahead), K and V row-major;
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: lane l holds scores of query
 //    l % 32 for 16 keys (lane l ^ 32 the other 16);
 //  * int8 and int4 K/V values q * s are rounded once to fp16 in the decode;
@@ -418,8 +432,9 @@ __device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, i
 //    stay <= 256), so the output rescale is rare; the row sum adds the fp16
 //    probabilities with v_dot2_f32_f16;
 //  * O^T += V^T P^T reuses the score registers as the B operand (the k order
-//    of an MFMA only has to agree between A and B: V^T is read in the score
-//    accumulator's key order 8*(i/4) + 4*(l/32) + i%4).
+//    of an MFMA only has to agree between A and B: V^T is read, with
+//    transposing LDS loads, in the score accumulator's key order
+//    8*(i/4) + 4*(l/32) + i%4).
 // Evicted/absent keys have score 0; they are added to the softmax
 // denominator at the end (n_ev * 2^(0 - m)).
 // ---------------------------------------------------------------------------
@@ -439,10 +454,10 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   constexpr int DPT = C::DPT, RW = C::RW > 0 ? C::RW : 1;
-  constexpr int VP = C::VPITCH;
+  constexpr int VR = C::VROW;
   // Two tile buffers: tile t+1 is decoded into one while tile t is multiplied from the other.
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][BN][D + KPAD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D][VP];
+  __shared__ __attribute__((aligned(16))) _Float16 Vs[2][BN][VR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -683,15 +698,17 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
           *reinterpret_cast<uint32_t*>(&Ks[buf][4 * kg + i][d0]) = kw[i][0];
         }
       }
-      // V^T rows d0 + e hold keys 4*kg .. 4*kg+3 (8 bytes): transpose the pair words.
+      // V rows like K rows (tile_pv reads them transposed)
 #pragma unroll
-      for (int x = 0; x < RW; ++x) {
-        *reinterpret_cast<uint2*>(&Vt[buf][d0 + 2 * x][4 * kg]) =
-            make_uint2(__builtin_amdgcn_perm(vw[1][x], vw[0][x], 0x05040100u),
-                       __builtin_amdgcn_perm(vw[3][x], vw[2][x], 0x05040100u));
-        *reinterpret_cast<uint2*>(&Vt[buf][d0 + 2 * x + 1][4 * kg]) =
-            make_uint2(__builtin_amdgcn_perm(vw[1][x], vw[0][x], 0x07060302u),
-                       __builtin_amdgcn_perm(vw[3][x], vw[2][x], 0x07060302u));
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DPT == 8) {
+          *reinterpret_cast<uint4*>(&Vs[buf][4 * kg + i][d0]) =
+              make_uint4(vw[i][0], vw[i][1], vw[i][2], vw[i][3]);
+        } else if constexpr (DPT == 4) {
+          *reinterpret_cast<uint2*>(&Vs[buf][4 * kg + i][d0]) = make_uint2(vw[i][0], vw[i][1]);
+        } else {
+          *reinterpret_cast<uint32_t*>(&Vs[buf][4 * kg + i][d0]) = vw[i][0];
+        }
       }
     }
   };
@@ -702,7 +719,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     uint32_t pw[16];
     tile_qk<D>(Ks[buf], qf, col, grp, m_run, sacc);
     tile_softmax<D>(sacc, nv, grp, m_run, l_run, o, pw);
-    tile_pv<D>(Vt[buf], pw, col, grp, o);
+    tile_pv<D>(Vs[buf], pw, col, grp, o);
     __builtin_amdgcn_s_setprio(0);
   };
 
