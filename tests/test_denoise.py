@@ -665,7 +665,8 @@ def test_shape_validation_without_gpu():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,S,H,D,group", [(1, 96, 4, 128, 16), (2, 67, 3, 64, 16),
                                            (1, 300, 2, 128, 32), (2, 33, 5, 64, 8),
-                                           (1, 1, 1, 128, 16)])
+                                           (1, 1, 1, 128, 16), (1, 2048, 32, 128, 16),
+                                           (2, 1000, 32, 128, 16)])
 def test_pack_projection_equals_rope_then_pack(dev, dtype, B, S, H, D, group):
     """PackedKVCache.pack_projection (K and V read from the q|k|v projection,
     K rotated in the pack kernel) writes the buckets and scales that
