@@ -473,7 +473,8 @@ int si_kv_pack_rope_flat(const void* qkv, const void* cos_table, const void* sin
  * and the down INT8Linear's activation quantization (int8_linear.py:96-98):
  * gate_up [M, 2F] (gate | up) in dtype; h = T(T(silu(g)) * u) [M, F]
  * (optional) with silu(g) = g / (1 + expf(-g)) in fp32 as torch computes it,
- * q int8 [M, F], scale fp32 [M]. F % 8 == 0, F <= 16384. */
+ * q int8 [M, F], scale fp32 [M]. F % 8 == 0, F <= 16384. For bf16 and fp16 the
+ * first call on a device also fills a 256 KB silu table in module memory. */
 int si_swiglu_quant(const void* gate_up, int dtype, int64_t M, int64_t F, void* h, int8_t* q,
                     float* scale, si_stream_t stream);
 

@@ -4,6 +4,8 @@
 // the down projection's activation quantization, and the per-position argmax /
 // confidence of the unmasking schedule (execution/block_decoding.py:148-151).
 // Every row kernel holds its row in registers: one read of HBM per element.
+#include <mutex>
+
 #include "si_common.h"
 
 namespace si {
@@ -296,12 +298,25 @@ __device__ __forceinline__ float silu_rounded(float g) {
   }
 }
 
+// silu_rounded<T>(x) for all 2^16 bf16 (row 0) and fp16 (row 1) bit patterns
+// x, as bits of T: a 16-bit row value picks its entry instead of evaluating
+// silu. Filled on a device (silu_table_fill, 65,536 threads) before its first
+// use; 256 KB of module memory per device, kept until the process ends.
+__device__ uint16_t silu_tab[2][65536];
+
+__global__ __launch_bounds__(256) void silu_table_fill() {
+  const uint32_t x = blockIdx.x * 256u + threadIdx.x;
+  silu_tab[0][x] = (uint16_t)f32_to_bf16_bits(silu_rounded<SI_DT_BF16>(bf16_bits_to_f32(x)));
+  silu_tab[1][x] = (uint16_t)f32_to_f16_bits(silu_rounded<SI_DT_F16>(f16_bits_to_f32(x)));
+}
+
 // ---------------------------------------------------------------------------
 // SwiGLU + down-projection input quantization (DiffusionLlamaMLP.forward,
 // diffusion_llama.py:332-333; the down INT8Linear prologue int8_linear.py:96-98):
 // gu [M, 2F] holds gate | up; h = T(T(silu(g)) * u) (torch's two elementwise
-// ops, each rounded to T; silu as silu_rounded). Writes h [M, F]
-// (optional) and its INT8Linear quantization q int8 [M, F], scale fp32 [M].
+// ops, each rounded to T; T(silu(g)) as silu_rounded, from silu_tab for bf16
+// and fp16 rows). Writes h [M, F] (optional) and its INT8Linear quantization
+// q int8 [M, F], scale fp32 [M].
 // ---------------------------------------------------------------------------
 template <int DT, int R>
 __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu, int64_t M, int F,
@@ -315,12 +330,25 @@ __global__ __launch_bounds__(256) void swiglu_quant(const void* __restrict__ gu,
     for (int r = 0; r < R; ++r) {
       const int c = (int)threadIdx.x + r * 256;
       if (c < nch) {
-        float g[8], u[8];
-        load8<DT>(gu, m * 2 * F + (int64_t)c * 8, g);
+        float u[8];
         load8<DT>(gu, m * 2 * F + F + (int64_t)c * 8, u);
+        if constexpr (DT == SI_DT_F32) {
+          float g[8];
+          load8<DT>(gu, m * 2 * F + (int64_t)c * 8, g);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          v[r][e] = round_to(silu_rounded<DT>(g[e]) * u[e], DT);
+          for (int e = 0; e < 8; ++e) v[r][e] = round_to(silu_rounded<DT>(g[e]) * u[e], DT);
+        } else {
+          const uint4 gw = *reinterpret_cast<const uint4*>(
+              reinterpret_cast<const uint16_t*>(gu) + m * 2 * F + (int64_t)c * 8);
+          const uint32_t ws[4] = {gw.x, gw.y, gw.z, gw.w};
+          const uint16_t* tab = silu_tab[DT == SI_DT_BF16 ? 0 : 1];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t bits = (e & 1) ? ws[e >> 1] >> 16 : ws[e >> 1] & 0xffffu;
+            const uint32_t sb = tab[bits];
+            const float sv = DT == SI_DT_BF16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
+            v[r][e] = round_to(sv * u[e], DT);
+          }
         }
         if (h != nullptr) store8<DT>(h, m * F + (int64_t)c * 8, v[r]);
       } else {
@@ -551,8 +579,39 @@ int rmsnorm_entry(const char* name, const void* x, const void* res, int dtype, i
   return check_launch(name);
 }
 
+// silu_tab is filled on a device by silu_table_fill launched on the stream
+// of every call until one fill is known to have finished (an event recorded
+// after it has completed); from then on every stream of the device reads the
+// table. Fills write identical values, so overlapping ones are harmless, and a
+// call under graph capture captures its fill.
+constexpr int kMaxDevices = 64;
+
+void ensure_silu_table(hipStream_t st) {
+  static std::mutex mu;
+  static bool ready[kMaxDevices];
+  static hipEvent_t done[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev >= kMaxDevices) dev = -1;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= 0 && ready[dev]) return;
+  if (dev >= 0 && !capturing && done[dev] != nullptr && hipEventQuery(done[dev]) == hipSuccess) {
+    ready[dev] = true;
+    return;
+  }
+  silu_table_fill<<<256, 256, 0, st>>>();
+  if (dev < 0 || capturing) return;
+  if (done[dev] == nullptr &&
+      hipEventCreateWithFlags(&done[dev], hipEventDisableTiming) != hipSuccess)
+    done[dev] = nullptr;
+  if (done[dev] != nullptr) (void)hipEventRecord(done[dev], st);
+}
+
 template <int DT>
 void launch_swiglu(const void* gu, int64_t M, int F, void* h, int8_t* q, float* s, hipStream_t st) {
+  if (DT != SI_DT_F32) ensure_silu_table(st);
   const unsigned g = row_grid(M);
   if (F <= 2048) swiglu_quant<DT, 1><<<g, 256, 0, st>>>(gu, M, F, h, q, s);
   else if (F <= 4096) swiglu_quant<DT, 2><<<g, 256, 0, st>>>(gu, M, F, h, q, s);

@@ -369,6 +369,46 @@ def test_swiglu_kernel(dev, dtype, M, F):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_swiglu_every_gate_value(dev, dtype):
+    """Every one of the 2^16 gate bit patterns (NaN and inf included) with
+    up = 1 and up = -3: h equals torch's silu(gate) * up on the GPU bit for
+    bit, NaN where torch gives NaN."""
+    from shadowinfer_amd.execution import row_ops
+    F = 8192
+    gate = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(dtype).view(8, F)
+    for up_val in (1.0, -3.0):
+        up = torch.full((8, F), up_val, dtype=dtype)
+        gd = torch.cat([gate, up], 1).to(dev)
+        h, _, _ = row_ops.swiglu_quant(gd, want_h=True)
+        want = torch.nn.functional.silu(gd[:, :F]) * gd[:, F:]
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(h), nan)
+        assert torch.equal(h[~nan], want[~nan])
+
+
+@pytest.mark.gpu
+def test_swiglu_under_graph_capture(dev):
+    """swiglu_quant captured in a HIP graph: three replays, with eager work
+    and a synchronization between them, each equal to the eager call."""
+    from shadowinfer_amd.execution import row_ops
+    g = torch.Generator().manual_seed(7)
+    gu = (torch.randn(64, 2 * 1024, generator=g) * 3).to(torch.bfloat16).to(dev)
+    h0, q0, s0 = row_ops.swiglu_quant(gu, want_h=True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        h, q, s = row_ops.swiglu_quant(gu, want_h=True)
+    for _ in range(3):
+        for t in (h, q, s):
+            t.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(h, h0) and torch.equal(q, q0) and torch.equal(s, s0)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("M,V,scale", [(3, 1, 1.0), (5, 7, 1.0), (64, 32000, 0.05),
                                        (64, 32000, 4.0), (2, 50001, 1.0), (33, 1000, 0.02)])
