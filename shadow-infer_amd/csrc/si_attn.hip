@@ -150,6 +150,7 @@ struct AttnCfg {
 };
 
 typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -215,6 +216,48 @@ __device__ __forceinline__ bool h_exact(uint32_t bits, float s) {
   return s >= 6.103515625e-05f && s * qmax <= 65504.0f && (float)(_Float16)s == s;
 }
 
+// The fp16 pair {s, s} of a scale that passed h_exact. A bf16 scale in that
+// range is a normal fp16 value with the same 7-bit significand, so its fp16
+// bits are its bf16 bits with the exponent rebiased from 127 to 15:
+// (bits << 3) - (112 << 10), formed in 32 bits (one shift-add) and splatted
+// from the low half. fp16 scales are their bits; fp32 scales are converted
+// (exactly).
+template <int SDT>
+__device__ __forceinline__ h2 scale_h2(uint32_t bits, float s) {
+  if constexpr (SDT == SI_DT_F32) {
+    const _Float16 h = (_Float16)s;
+    return h2{h, h};
+  } else {
+    const uint32_t w = SDT == SI_DT_BF16 ? (bits << 3) - 0x1C000u : bits;
+    const h2 p = __builtin_bit_cast(h2, w);
+    return __builtin_shufflevector(p, p, 0, 0);
+  }
+}
+
+// The two halves of a wave exchanged with v_permlane32_swap_b32 (a VALU op,
+// no LDS round trip): lane l receives the value of lane l ^ 32 in one of the
+// two results and keeps its own in the other, so max / sum of the pair is the
+// pair's max / sum in every lane. The elements are read into scalars before
+// the bit cast: clang lowers __builtin_bit_cast of a vector element lvalue
+// as a load of element 0.
+__device__ __forceinline__ void halves_swap(float v, float& x, float& y) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const v2u r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r.x, r1 = r.y;
+  x = __builtin_bit_cast(float, r0);
+  y = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float halves_max(float v) {
+  float x, y;
+  halves_swap(v, x, y);
+  return fmaxf(x, y);
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  float x, y;
+  halves_swap(v, x, y);
+  return x + y;
+}
+
 // ---------------------------------------------------------------------------
 // The three parts of one 64-key tile for the 32 queries of a wave.
 //
@@ -227,13 +270,8 @@ __device__ __forceinline__ bool h_exact(uint32_t bits, float s) {
 // ready, the one feeding the matrix core issues first.
 template <int D>
 __device__ __forceinline__ void tile_qk(const _Float16 (*Ks)[D + KPAD], const v8h* qf, int col,
-                                        int grp, float m_run, v16f (&sacc)[2]) {
+                                        int grp, const v16f& cinit, v16f (&sacc)[2]) {
   constexpr int KS = D / 16;
-  const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[kb][r] = c0;
   v8h ka[2][2];
   auto load_k = [&](int ks, v8h* a) __attribute__((always_inline)) {
     a[0] = *reinterpret_cast<const v8h*>(&Ks[col][ks * 16 + 8 * grp]);
@@ -244,8 +282,8 @@ __device__ __forceinline__ void tile_qk(const _Float16 (*Ks)[D + KPAD], const v8
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     if (ks + 1 < KS) load_k(ks + 1, ka[(ks + 1) & 1]);
-    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][0], qf[ks], sacc[0], 0, 0, 0);
-    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][1], qf[ks], sacc[1], 0, 0, 0);
+    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][0], qf[ks], ks == 0 ? cinit : sacc[0], 0, 0, 0);
+    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks & 1][1], qf[ks], ks == 0 ? cinit : sacc[1], 0, 0, 0);
     if (ks + 1 < KS) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two reads of ks+1
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // then the two MFMAs of ks
@@ -261,7 +299,8 @@ __device__ __forceinline__ void tile_qk(const _Float16 (*Ks)[D + KPAD], const v8
 // fp16 values in fp32 (v_dot2_f32_f16 with {1, 1}).
 template <int D>
 __device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, float& m_run,
-                                             float& l_run, v16f* o, uint32_t (&pw)[16]) {
+                                             v16f& cinit, float& l_run, v16f* o,
+                                             uint32_t (&pw)[16]) {
   constexpr int DB = D / 32;
   const float c0 = m_run == -INFINITY ? 0.0f : -m_run;
   if (nv < BN) {
@@ -277,7 +316,7 @@ __device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, f
 #pragma unroll
     for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], sacc[kb][r]);
   float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = halves_max(tmax);
   const bool raise = m_run == -INFINITY || tmax > 8.0f;
   if (__builtin_amdgcn_ballot_w64(raise) != 0) {
     const float m_new = raise ? tmax - c0 : m_run;
@@ -293,6 +332,8 @@ __device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, f
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kb][r] -= delta;
     m_run = m_new;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cinit[r] = m_new == -INFINITY ? 0.0f : -m_new;
   }
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -307,8 +348,7 @@ __device__ __forceinline__ void tile_softmax(v16f (&sacc)[2], int nv, int grp, f
   const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
   for (int w = 0; w < 16; ++w) ps[w & 3] = __builtin_amdgcn_fdot2(as_h2(pw[w]), ones, ps[w & 3], false);
-  const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
-  l_run += psum + __shfl_xor(psum, 32, 64);
+  l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);  // this half's keys; halves added at the end
 }
 
 // tile_pv: O^T += V^T P^T over four 16-key chunks. The score registers are
@@ -376,6 +416,7 @@ template <int D>
 __device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, int n_ev,
                                             bool m_ok, int64_t obase, int grp, void* O, int odt) {
   constexpr int DB = D / 32;
+  l_run = halves_sum(l_run);  // each half summed its own keys
   if (n_ev > 0) {
     const float m_fin = fmaxf(m_run, 0.0f);
     const float alpha = exp2f(m_run - m_fin);
@@ -443,8 +484,10 @@ struct OutStrides {
   int64_t b, h, s;
 };
 
-// O32: every bucket and scale buffer is below 2^31 bytes, so row addresses are
-// 32-bit byte offsets from the (uniform) buffer base.
+// O32: every bucket and scale buffer is below 2^31 bytes and B * D < 2^21, so
+// row addresses are 32-bit byte offsets from the (uniform) buffer base, and
+// the full-rate 24-bit multiply forms them: slots are below 2^23 (n_max * B *
+// D * 4 < 2^31 with B * D >= 64) and every row stride below 2^24.
 template <int D, int SDT, int QDT, bool O32>
 __global__ __launch_bounds__(512) void attn_packed_fwd(
     const uint16_t* __restrict__ Q, int64_t B, int64_t H, int64_t Sq, int64_t cap,
@@ -533,19 +576,20 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
       const int sli = 4 * kg + i < nv ? sl4[i] : 0;
       if constexpr (O32) {
         const uint32_t us = (uint32_t)sli;
+        __builtin_assume(us < (1u << 23));
         if constexpr (P == SI_PREC_FP16) {
-          load_raw<2 * DPT>(at(4, us * st16 + c16), rk[i]);
-          load_raw<2 * DPT>(at(5, us * st16 + c16), rv[i]);
+          load_raw<2 * DPT>(at(4, __umul24(us, st16) + c16), rk[i]);
+          load_raw<2 * DPT>(at(5, __umul24(us, st16) + c16), rv[i]);
         } else if constexpr (P == SI_PREC_INT8) {
-          load_raw<DPT>(at(8, us * st8 + c8), rk[i]);
-          load_raw<DPT>(at(9, us * st8 + c8), rv[i]);
-          load_raw<SS>(at(10, us * st8s + c8s), &skb[i]);
-          load_raw<SS>(at(11, us * st8s + c8s), &svb[i]);
+          load_raw<DPT>(at(8, __umul24(us, st8) + c8), rk[i]);
+          load_raw<DPT>(at(9, __umul24(us, st8) + c8), rv[i]);
+          load_raw<SS>(at(10, __umul24(us, st8s) + c8s), &skb[i]);
+          load_raw<SS>(at(11, __umul24(us, st8s) + c8s), &svb[i]);
         } else if constexpr (P == SI_PREC_INT4) {
-          load_raw<DPT / 2>(at(12, us * st4 + c4), rk[i]);
-          load_raw<DPT / 2>(at(13, us * st4 + c4), rv[i]);
-          load_raw<SS>(at(14, us * st4s + c4s), &skb[i]);
-          load_raw<SS>(at(15, us * st4s + c4s), &svb[i]);
+          load_raw<DPT / 2>(at(12, __umul24(us, st4) + c4), rk[i]);
+          load_raw<DPT / 2>(at(13, __umul24(us, st4) + c4), rv[i]);
+          load_raw<SS>(at(14, __umul24(us, st4s) + c4s), &skb[i]);
+          load_raw<SS>(at(15, __umul24(us, st4s) + c4s), &svb[i]);
         }
         continue;
       }
@@ -576,6 +620,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
   float m_run = -INFINITY;
+  v16f cinit = {};  // the QK accumulators' start value: -m_run (0 before the first raise)
   float l_run = 0.0f;
 
   // Decode tile tt (its rows are in rk / rv) into LDS buffer buf.
@@ -646,7 +691,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         if (__builtin_amdgcn_ballot_w64(fast == 0) == 0) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const h2 k2 = {(_Float16)sk[i], (_Float16)sk[i]}, v2 = {(_Float16)sv[i], (_Float16)sv[i]};
+            const h2 k2 = scale_h2<SDT>(skb[i], sk[i]), v2 = scale_h2<SDT>(svb[i], sv[i]);
 #pragma unroll
             for (int x = 0; x < RW; ++x) {
               kw[i][x] = as_u32(as_h2(kw[i][x]) * k2);
@@ -717,8 +762,8 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   auto compute_tile = [&](int nv, int buf) __attribute__((always_inline)) {
     v16f sacc[2];
     uint32_t pw[16];
-    tile_qk<D>(Ks[buf], qf, col, grp, m_run, sacc);
-    tile_softmax<D>(sacc, nv, grp, m_run, l_run, o, pw);
+    tile_qk<D>(Ks[buf], qf, col, grp, cinit, sacc);
+    tile_softmax<D>(sacc, nv, grp, m_run, cinit, l_run, o, pw);
     tile_pv<D>(Vs[buf], pw, col, grp, o);
     __builtin_amdgcn_s_setprio(0);
   };
@@ -787,7 +832,8 @@ void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t 
                  const OutStrides& os, int64_t n_max) {
   // SI_ATTN_OFFSET64 (any value) selects the 64-bit addressing at every size, so tests can
   // compare the two paths on small caches.
-  if (n_max * B * D * 4 < ((int64_t)1 << 31) && getenv("SI_ATTN_OFFSET64") == nullptr)
+  if (n_max * B * D * 4 < ((int64_t)1 << 31) && B * D < ((int64_t)1 << 21) &&
+      getenv("SI_ATTN_OFFSET64") == nullptr)
     launch_attn_o<D, QDT, true>(sdt, grid, st, q, B, H, Sq, cap, counts, lists, bk, g, scale_log2,
                                 out, odt, os);
   else

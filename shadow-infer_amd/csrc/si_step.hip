@@ -590,14 +590,20 @@ void ensure_silu_table(hipStream_t st) {
   static std::mutex mu;
   static bool ready[kMaxDevices];
   static hipEvent_t done[kMaxDevices];
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev >= kMaxDevices) dev = -1;
+  static bool recorded[kMaxDevices];  // a never-recorded event reads as complete
+  // The stream's device; -1 (fill on every call, no event) when it is not the
+  // current device, where an event created here could not be recorded on st.
+  hipDevice_t dev = -1;
+  int cur = -1;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess || hipGetDevice(&cur) != hipSuccess ||
+      dev != cur || dev < 0 || dev >= kMaxDevices)
+    dev = -1;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   const bool capturing =
       hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> lock(mu);
   if (dev >= 0 && ready[dev]) return;
-  if (dev >= 0 && !capturing && done[dev] != nullptr && hipEventQuery(done[dev]) == hipSuccess) {
+  if (dev >= 0 && !capturing && recorded[dev] && hipEventQuery(done[dev]) == hipSuccess) {
     ready[dev] = true;
     return;
   }
@@ -606,7 +612,7 @@ void ensure_silu_table(hipStream_t st) {
   if (done[dev] == nullptr &&
       hipEventCreateWithFlags(&done[dev], hipEventDisableTiming) != hipSuccess)
     done[dev] = nullptr;
-  if (done[dev] != nullptr) (void)hipEventRecord(done[dev], st);
+  if (done[dev] != nullptr && hipEventRecord(done[dev], st) == hipSuccess) recorded[dev] = true;
 }
 
 template <int DT>
