@@ -567,13 +567,18 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     tt = min(tt, t_last);
     const int nv = __builtin_amdgcn_readfirstlane(tile_valid(tt, P));
     sl_data = sl;
-    const int sl4[4] = {sl.x, sl.y, sl.z, sl.w};
+    int sl4[4] = {sl.x, sl.y, sl.z, sl.w};
     if constexpr (P == SI_PREC_FP32) return;  // read at decode time
+    // Keys past the tile's valid count (only in a phase's last tile: nv is
+    // wave-uniform) read row 0 of the same (non-empty) bucket: their list
+    // entries are not written, and their scores are masked to -inf.
+    if (nv < BN) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sl4[i] = 4 * kg + i < nv ? sl4[i] : 0;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // Keys past the tile's valid count read row 0 of the same (non-empty)
-      // bucket: their scores are masked to -inf, so they contribute nothing.
-      const int sli = 4 * kg + i < nv ? sl4[i] : 0;
+      const int sli = sl4[i];
       if constexpr (O32) {
         const uint32_t us = (uint32_t)sli;
         __builtin_assume(us < (1u << 23));
