@@ -7,11 +7,12 @@
 // (models/simple_diffusion_llm.py:165-169). The dense K/V never exist: each
 // 64-token tile is dequantized straight into LDS as fp16.
 //
-// Work split: one block of 4 wavefronts owns 128 queries of one (b, h); each
-// wave owns 32 queries. Per 64-key tile a wave computes S^T = K Q^T with
-// v_mfma_f32_32x32x16_f16, so lane l holds scores of query (l % 32) for 16 of
-// the tile's keys and lane l ^ 32 the other 16: the online-softmax max and sum
-// need one cross-lane shuffle. O^T = V^T P^T then reuses the score registers
+// Work split: one block of 8 wavefronts (two per SIMD) owns 256 queries of one
+// (b, h); each wave owns 32 queries. Per 64-key tile a wave computes S^T = K Q^T
+// with v_mfma_f32_32x32x16_f16, so lane l holds scores of query (l % 32) for 16
+// of the tile's keys and lane l ^ 32 the other 16: the online-softmax max takes
+// one exchange of the wave halves per tile, and each half keeps its own row sum
+// until the last tile. O^T = V^T P^T then reuses the score registers
 // as the B operand; the k order of an MFMA only has to match between its A and
 // B operands, so V^T is read from LDS (V row-major, read with the transposing
 // ds_read_b64_tr_b16) in the key order the score accumulator already has
