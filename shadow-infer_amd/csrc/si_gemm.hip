@@ -275,12 +275,25 @@ __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// DMA tile kernel: global -> LDS copies by global_load_lds_dwordx4 (no register
-// staging) into S LDS stages, so k-tiles t+1 .. t+S-2 are in flight while the
-// MFMAs of k-tile t run. One wave instruction fills 1 KB of LDS, lane l the
-// 16 bytes at 16*l: rows of a stage are therefore unpadded (BK bytes) and the
-// 16-byte chunks of row r are stored at slot chunk ^ swz(r); swz spreads the
-// rows read by one fragment load over distinct banks.
+// DMA tile kernel: global -> LDS copies by buffer_load_dwordx4 ... lds (no
+// register staging). The A part of each k-tile (BM x BK) goes to one of RA LDS
+// slots and the B part (BN x BK) to one of RB slots; iteration t issues A(t +
+// RA - 1) and B(t + RB - 1), so B runs RB - 1 k-tiles ahead. One wave
+// instruction fills 1 KB of LDS, lane l the 16 bytes at 16*l: rows of a slot
+// are therefore unpadded (BK bytes) and the 16-byte chunks of row r are stored
+// at slot chunk ^ swz(r); swz spreads the rows read by one fragment load over
+// distinct banks.
+//
+// Why the B ring is deeper: a CU fills its LDS at (L1->L2 reads in flight) x
+// 128 B / latency, and the TCP holds only about 90 reads in flight. With two
+// whole stages of a 256x192x128 tile (the LDS holds no third) the queue of
+// copies ran dry at every k-tile boundary (about 70 reads in flight on
+// average, 20 B per clock at 4096 x 11008, M = 1024). With A in 2 slots and B
+// in 4 (160 KB), the weight rows of the next three k-tiles stay queued across
+// the barrier: 87 in flight, 25.5 B per clock, and the loop 11% shorter.
+// A resource descriptor with the exact buffer size per operand makes the
+// copies 32-bit offsets from one scalar base (about 5% faster than 64-bit
+// global_load_lds addresses) and bounds every read by the hardware.
 //
 // MFMA fragments are double-buffered in registers: the loads for k-slice s+1
 // are issued between the MFMAs of k-slice s, and the first k-slice of k-tile
@@ -298,6 +311,15 @@ __global__ __launch_bounds__(256) void gemm_tile(const int8_t* __restrict__ A,
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
+
+// 16 bytes per lane from byte `off` of a raw buffer of `bytes` bytes into LDS
+// (buffer_load_dwordx4 ... lds; data format 32-bit, reads past `bytes` give 0).
+__device__ __forceinline__ void buf_copy16(const void* base, uint32_t bytes, lvoid_t* dst,
+                                           uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, off, 0, 0, 0);
+}
 
 template <int CPR>
 __device__ __forceinline__ int chunk_swz(int r) {
@@ -511,27 +533,32 @@ __device__ __forceinline__ void store_frag_row(const v16i* acc, int m_base, int 
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int S, int EPI>
+template <int BM, int BN, int BK, int WM, int WN, int RA, int RB, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restrict__ A,
                                                          const int8_t* __restrict__ B, int M,
                                                          int N, int K, int k_split,
                                                          int32_t* __restrict__ Cout, EpiArgs ep) {
   constexpr int NW = WM * WN;  // 4 waves (one per SIMD) or 8 (two per SIMD)
   static_assert(NW == 4 || NW == 8, "four or eight waves per block");
+  static_assert(RA >= 2 && (RA == RB || (RA == 2 && RB > 2)), "equal rings, or A in 2 slots");
   constexpr int CPR = BK / 16;
   constexpr int LA = BM * BK / 1024 / NW;  // 1-KB DMA blocks of A per wave per k-tile
   constexpr int LB = BN * BK / 1024 / NW;
   static_assert(LA * 1024 * NW == BM * BK && LB * 1024 * NW == BN * BK, "whole DMA blocks per wave");
   constexpr int LPT = LA + LB;        // vm loads per thread per k-tile
-  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int ASZ = BM * BK, BSZ = BN * BK;
+  constexpr int LDS_BYTES = RA * ASZ + RB * BSZ;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
   static_assert(FM * 32 == TM && FN * 32 == TN, "32-row fragments");
   constexpr int KS = BK / 32;
   static_assert(KS % 2 == 0, "fragment buffers alternate per k-slice");
   constexpr int EP = TN + 8;  // epilogue staging pitch in words (rows r and r+4 on other banks)
-  static_assert(NW * 16 * EP * 4 <= S * STAGE, "epilogue staging fits in the stages");
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+  static_assert(NW * 16 * EP * 4 <= LDS_BYTES, "epilogue staging fits in the rings");
+  static_assert(RA == RB ? (RA - 2) * LPT <= 63 : (RB - 2) * LB <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+  int8_t* const ldsA = lds;
+  int8_t* const ldsB = lds + RA * ASZ;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -548,16 +575,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
   const int ke = min(kb + k_split, K);
   const int nk = (ke - kb) / BK;
 
-  // Source of the 16 bytes this lane copies into each of its DMA blocks.
-  const int8_t* asrc[LA];
-  const int8_t* bsrc[LB];
+  // Byte offset of the 16 bytes this lane copies into each of its DMA blocks
+  // (operands are below 2^31 bytes; the host checks).
+  const uint32_t abytes = (uint32_t)M * (uint32_t)K, bbytes = (uint32_t)N * (uint32_t)K;
+  uint32_t aoff[LA], boff[LB];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
     const int p = (i * NW + wave) * 1024 + 16 * lane;
     const int r = p / BK;
     const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
     const int m = min(m0 + r, M - 1);  // rows past M feed only discarded outputs
-    asrc[i] = A + (int64_t)m * K + kb + 16 * c;
+    aoff[i] = (uint32_t)m * (uint32_t)K + (uint32_t)(kb + 16 * c);
   }
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
@@ -565,19 +593,34 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
     const int r = p / BK;
     const int c = ((p % BK) / 16) ^ chunk_swz<CPR>(r);
     const int n = min(n0 + r, N - 1);
-    bsrc[i] = B + (int64_t)n * K + kb + 16 * c;
+    boff[i] = (uint32_t)n * (uint32_t)K + (uint32_t)(kb + 16 * c);
   }
-  auto issue = [&](int t) {
-    int8_t* st = lds + (t % S) * STAGE;
-    const int k0 = t * BK;
+  auto issueA = [&](int t) {
+    int8_t* st = ldsA + (t % RA) * ASZ;
 #pragma unroll
     for (int i = 0; i < LA; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid_t*)(asrc[i] + k0),
-                                       (lvoid_t*)(st + (i * NW + wave) * 1024), 16, 0, 0);
+      buf_copy16(A, abytes, (lvoid_t*)(st + (i * NW + wave) * 1024), aoff[i] + (uint32_t)(t * BK));
+  };
+  auto issueB = [&](int t) {
+    int8_t* st = ldsB + (t % RB) * BSZ;
 #pragma unroll
     for (int i = 0; i < LB; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid_t*)(bsrc[i] + k0),
-                                       (lvoid_t*)(st + BM * BK + (i * NW + wave) * 1024), 16, 0, 0);
+      buf_copy16(B, bbytes, (lvoid_t*)(st + (i * NW + wave) * 1024), boff[i] + (uint32_t)(t * BK));
+  };
+  // This wave's copies of A(t+1) and B(t+1) have landed and its LDS reads are
+  // complete (called at the end of iteration t; t = -1 before the loop).
+  auto wait_next = [&](int t) {
+    if constexpr (RA == RB) {
+      // iteration u issued A(u+RA-1), B(u+RA-1): up to RA-2 later k-tiles may fly
+      wait_tiles<LPT, RA>(min(nk - 2 - t, RA - 2));
+    } else if (t < 0) {
+      // prologue issued A(0), B(0), then B(1) .. B(RB-2)
+      wait_tiles<LB, RB>(min(nk - 1, RB - 2));
+    } else {
+      // iteration t issued A(t+1), then B(t+RB-1) (if any), which may fly
+      if (t + RB - 1 < nk) wait_cnt<LB, 0>();
+      else wait_cnt<0, 0>();
+    }
   };
 
   v16i acc[FM][FN];
@@ -599,44 +642,51 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int r = wn * TN + j * 32 + (lane & 31);
-    brow[j] = BM * BK + r * BK;
+    brow[j] = r * BK;
     bsw[j] = chunk_swz<CPR>(r);
   }
   const int khalf = lane >> 5;
   v4i af[2][FM], bf[2][FN];
-  auto load_frags = [&](const int8_t* st, int ks, v4i* a, v4i* b) {
+  auto load_frags = [&](int t, int ks, v4i* a, v4i* b) {
+    const int8_t* sa = ldsA + (t % RA) * ASZ;
+    const int8_t* sb = ldsB + (t % RB) * BSZ;
     const int c = 2 * ks + khalf;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const v4i*>(st + arow[i] + 16 * (c ^ asw[i]));
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const v4i*>(sa + arow[i] + 16 * (c ^ asw[i]));
 #pragma unroll
-    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const v4i*>(st + brow[j] + 16 * (c ^ bsw[j]));
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const v4i*>(sb + brow[j] + 16 * (c ^ bsw[j]));
   };
 
   if (nk > 0) {
-    for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
-    wait_tiles<LPT, S>(min(nk - 1, S - 2));
+    // A(0 .. RA-2) and B(0 .. RB-2), in k order, A before B
+#pragma unroll
+    for (int j = 0; j < RB - 1; ++j) {
+      if (j < RA - 1 && j < nk) issueA(j);
+      if (j < nk) issueB(j);
+    }
+    wait_next(-1);
     bare_barrier();
-    load_frags(lds, 0, af[0], bf[0]);
+    load_frags(0, 0, af[0], bf[0]);
   }
   for (int t = 0; t < nk; ++t) {
-    // Stage (t-1) % S is free: every wave passed the barrier of k-tile t-1's
-    // last k-slice after its reads of k-tile t-1 had completed.
-    if (t + S - 1 < nk) issue(t + S - 1);
-    const int8_t* st = lds + (t % S) * STAGE;
+    // The slots of k-tile t-1 are free: every wave passed the barrier of
+    // k-tile t-1's last k-slice after its reads of k-tile t-1 had completed.
+    if (t + RA - 1 < nk) issueA(t + RA - 1);
+    if (t + RB - 1 < nk) issueB(t + RB - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int cur = ks & 1;
       if (ks + 1 < KS) {
-        load_frags(st, ks + 1, af[cur ^ 1], bf[cur ^ 1]);
+        load_frags(t, ks + 1, af[cur ^ 1], bf[cur ^ 1]);
       } else {
         // k-tile t+1: this wave's copies have landed and its reads of k-tile
         // t are complete; after the barrier the same holds for every wave.
         // Unconditional (branch-free, so the loads interleave with the MFMAs
-        // below): after the last k-tile it waits for nothing and reads a
-        // stale stage whose fragments are never used.
-        wait_tiles<LPT, S>(min(nk - 2 - t, S - 2));
+        // below): after the last k-tile it waits for nothing and reads
+        // stale slots whose fragments are never used.
+        wait_next(t);
         bare_barrier();
-        load_frags(lds + ((t + 1) % S) * STAGE, 0, af[cur ^ 1], bf[cur ^ 1]);
+        load_frags(t + 1, 0, af[cur ^ 1], bf[cur ^ 1]);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -1241,6 +1291,12 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     p.bm = 128; p.bn = 128; p.bk = K % 128 == 0 ? 128 : 32;
     if (K % 32 != 0) { p.kind = K_SCALAR; return p; }
   }
+  // gemm_dma addresses each operand with 32-bit byte offsets.
+  if (p.kind != K_TILE_128x128 && (M * K >= ((int64_t)1 << 31) || N * K >= ((int64_t)1 << 31))) {
+    p.kind = K_TILE_128x128;
+    p.bm = 128; p.bn = 128; p.bk = K % 128 == 0 ? 128 : 32;
+    if (K % 32 != 0) { p.kind = K_SCALAR; return p; }
+  }
   p.splits = 1;
   p.k_split = (int)K;
   int want = forced_splits();
@@ -1272,8 +1328,9 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
   // DMA kernels: one linear grid dimension over the tiles (renumbered per XCD
   // inside the kernel), splits in z.
   const dim3 grid((unsigned)(ceil_div(M, p.bm) * ceil_div(N, p.bn)), 1, (unsigned)p.splits);
-#define SI_DMA(BM_, BN_, BK_, WM_, WN_, S_)                                                    \
-  gemm_dma<BM_, BN_, BK_, WM_, WN_, S_, EPI><<<grid, dim3(64 * WM_ * WN_), 0, st>>>( \
+#define SI_DMA(BM_, BN_, BK_, WM_, WN_, S_) SI_DMA2(BM_, BN_, BK_, WM_, WN_, S_, S_)
+#define SI_DMA2(BM_, BN_, BK_, WM_, WN_, RA_, RB_)                                                \
+  gemm_dma<BM_, BN_, BK_, WM_, WN_, RA_, RB_, EPI><<<grid, dim3(64 * WM_ * WN_), 0, st>>>( \
       a, b, M, N, K, p.k_split, c, ep)
   switch (p.kind) {
     case K_DMA_256x256: SI_DMA(256, 256, 64, 2, 2, 4); break;
@@ -1282,10 +1339,10 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
     case K_DMA_128x128: SI_DMA(128, 128, 128, 2, 2, 4); break;
     case K_DMA_256x192: SI_DMA(256, 192, 64, 2, 2, 4); break;
     case K_DMA_256x64: SI_DMA(256, 64, 128, 4, 1, 3); break;
-    case K_DMA_256x128_K128: SI_DMA(256, 128, 128, 2, 2, 3); break;
+    case K_DMA_256x128_K128: SI_DMA2(256, 128, 128, 2, 2, 2, 6); break;
     case K_DMA8_256x256: SI_DMA(256, 256, 64, 4, 2, 4); break;
-    case K_DMA8_256x256_K128: SI_DMA(256, 256, 128, 4, 2, 2); break;
-    case K_DMA8_256x192_K128: SI_DMA(256, 192, 128, 4, 2, 2); break;
+    case K_DMA8_256x256_K128: SI_DMA2(256, 256, 128, 4, 2, 2, 3); break;
+    case K_DMA8_256x192_K128: SI_DMA2(256, 192, 128, 4, 2, 2, 4); break;
     case K_DMA8_256x128: SI_DMA(256, 128, 64, 4, 2, 4); break;
     case K_DMA8_128x128_42: SI_DMA(128, 128, 128, 4, 2, 4); break;
     case K_DMA8_128x128_24: SI_DMA(128, 128, 128, 2, 4, 4); break;
@@ -1295,6 +1352,7 @@ void launch_tile(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
     default: SI_DMA(128, 256, 64, 2, 4, 4); break;
   }
 #undef SI_DMA
+#undef SI_DMA2
 }
 
 template <int MF, int EPI>
