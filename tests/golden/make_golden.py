@@ -6,8 +6,9 @@ from the oracle: the quantizers of shadowinfer/utils/quantization.py:120-178
 bucket gather and int4 row packing of shadowinfer/shadowkv/packed_kv_cache.py:
 222-388 (token-major entries, gather index h*S+t, nibble q+8 high first, zero
 pad on odd rows), the plan fingerprint of shadowinfer/shadowkv/
-precision_plan.py:179-190, the evict compaction of packed_kv_cache.py:666-740
-and INT8Linear (shadowinfer/ffn_optimizer/int8_linear.py:65-115, the int32
+precision_plan.py:179-190, the evict compaction of packed_kv_cache.py:666-740,
+apply_reuse_mask (packed_kv_cache.py:753-854, restated over dense [S, H]
+maps of the previous cache's bucket and row) and INT8Linear (shadowinfer/ffn_optimizer/int8_linear.py:65-115, the int32
 product as an exact int64 matmul).
 
 Inputs come from a counter-based integer generator (splitmix64), so they are
@@ -152,6 +153,60 @@ def evict(packed, drop):
     return out, removed
 
 
+def reuse(cur, prev, mask, B):
+    """apply_reuse_mask (packed_kv_cache.py:753-854) over dense [S, H] maps.
+
+    ``pcode[t, h]`` is the bucket (0..3) that holds entry (t, h) in the
+    previous cache and ``ppos[t, h]`` its row there; both are -1 where the
+    previous cache holds no such entry (code 4, evicted after packing, or t at
+    or beyond its seq_len). A current entry whose mask is set takes the
+    previous row when the buckets agree; when the previous cache holds it in
+    another bucket it is counted as skipped; otherwise nothing happens. Row
+    copies are the reference's index_select + index_copy_. Returns the new
+    buckets and (applied, skipped_precision)."""
+    S, H = mask.shape
+    pcode = np.full((S, H), -1, np.int64)
+    ppos = np.full((S, H), -1, np.int64)
+    for p, name in enumerate(NAMES):
+        if name not in prev:
+            continue
+        ix = prev[name]["indices"].astype(np.int64)
+        inside = ix[:, 0] < S
+        pcode[ix[inside, 0], ix[inside, 1]] = p
+        ppos[ix[inside, 0], ix[inside, 1]] = np.nonzero(inside)[0]
+    out, applied, skipped = {}, 0, 0
+    for p, name in enumerate(NAMES):
+        if name not in cur:
+            continue
+        d = {key: (t.clone() if isinstance(t, torch.Tensor) else t.copy()) for key, t in cur[name].items()}
+        out[name] = d
+        ix = d["indices"].astype(np.int64)
+        sel = mask[ix[:, 0], ix[:, 1]]
+        pc = pcode[ix[:, 0], ix[:, 1]]
+        skipped += int((sel & (pc >= 0) & (pc != p)).sum())
+        tgt_np = np.nonzero(sel & (pc == p))[0]
+        if tgt_np.size == 0:
+            continue
+        applied += int(tgt_np.size)
+        tgt = torch.from_numpy(tgt_np)
+        src = torch.from_numpy(ppos[ix[tgt_np, 0], ix[tgt_np, 1]])
+        n, pn = len(ix), len(prev[name]["indices"])
+        for j in ("k", "v"):
+            if name == "int4":
+                rows = d[j].reshape(n, -1)
+                rows.index_copy_(0, tgt, prev[name][j].reshape(pn, -1).index_select(0, src))
+                d[j] = rows.reshape(-1)
+                G = d["scale_" + j].shape[1]
+                sc = d["scale_" + j].reshape(n, B, G, 1)
+                sc.index_copy_(0, tgt, prev[name]["scale_" + j].reshape(pn, B, G, 1).index_select(0, src))
+                d["scale_" + j] = sc.reshape(n * B, G, 1)
+            else:
+                d[j].index_copy_(0, tgt, prev[name][j].index_select(0, src))
+                if "scale_" + j in d:
+                    d["scale_" + j].index_copy_(0, tgt, prev[name]["scale_" + j].index_select(0, src))
+    return out, applied, skipped
+
+
 def raw(t):
     """Bytes of a tensor (bf16/fp16 as uint16, the rest as numpy)."""
     if t.dtype in (torch.bfloat16, torch.float16):
@@ -225,6 +280,41 @@ def config1_digests():
     }
 
 
+def reuse_case(path, B=2, H=4, S=24, S_prev=16, D=32, group=16, seed=400):
+    """apply_reuse_mask from a previous cache that is shorter (S_prev < S),
+    holds evicted entries (code 4, and entries evicted after packing) and puts
+    many entries in other buckets than the current cache, bf16 K/V. The mask
+    sets about 60% of the current token-heads, the rest are False."""
+    dt = torch.bfloat16
+    k = torch.from_numpy(gen_f32((B, H, S, D), seed, outlier_every=13)).to(dt)
+    v = torch.from_numpy(gen_f32((B, H, S, D), seed + 1)).to(dt)
+    kp = torch.from_numpy(gen_f32((B, H, S_prev, D), seed + 2, outlier_every=7)).to(dt)
+    vp = torch.from_numpy(gen_f32((B, H, S_prev, D), seed + 3)).to(dt)
+    codes = gen_codes(S, H, seed + 4)
+    # the previous step's codes: the current ones with about 40% redrawn
+    codes_prev = codes[:S_prev].copy()
+    redraw = gen_uniform(S_prev * H, seed + 8).reshape(S_prev, H) < 0.4
+    codes_prev[redraw] = gen_codes(S_prev, H, seed + 5)[redraw]
+    cur = pack(k, v, codes, group)
+    prev = pack(kp, vp, codes_prev, group)
+    present = [(int(t), int(h)) for t, h in zip(*np.nonzero(codes_prev != 4))]
+    pick = gen_uniform(len(present), seed + 6) < 0.2
+    drop = sorted(e for e, x in zip(present, pick) if x)
+    prev, removed = evict(prev, set(drop))
+    assert removed == len(drop)
+    mask = gen_uniform(S * H, seed + 7).reshape(S, H) < 0.6
+    out, applied, skipped = reuse(cur, prev, mask, B)
+    ko, vo = unpack(out, B, H, S, D, group)
+    arrays = {"k": raw(k), "v": raw(v), "k_prev": raw(kp), "v_prev": raw(vp), "codes": codes,
+              "codes_prev": codes_prev, "drop": np.array(drop, np.int32).reshape(-1, 2),
+              "mask": mask, "applied": np.int64(applied), "skipped_precision": np.int64(skipped),
+              "unpack_k": ko.numpy(), "unpack_v": vo.numpy()}
+    for name, d in out.items():
+        for key, t in d.items():
+            arrays[f"{name}.{key}"] = t if isinstance(t, np.ndarray) else raw(t)
+    np.savez_compressed(path, **arrays)
+
+
 def int8_linear_case(path, M=8, K=128, N=96, seed=300):
     w = torch.from_numpy(gen_f32((N, K), seed)) * 0.005
     x = torch.from_numpy(gen_f32((M, K), seed + 1)).to(torch.bfloat16)
@@ -248,6 +338,7 @@ def main():
     kv_case(os.path.join(HERE, "kv_bf16_b2h3s17d48.npz"), torch.bfloat16, 2, 3, 17, 48, 16, 21)
     kv_case(os.path.join(HERE, "kv_bf16_b1h2s9d45.npz"), torch.bfloat16, 1, 2, 9, 45, 16, 31)
     int8_linear_case(os.path.join(HERE, "int8_linear_m8k128n96.npz"))
+    reuse_case(os.path.join(HERE, "reuse_bf16_b2h4s24p16d32.npz"))
     with open(os.path.join(HERE, "config1_digests.json"), "w") as f:
         json.dump(config1_digests(), f, indent=1, sort_keys=True)
         f.write("\n")

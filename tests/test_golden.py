@@ -1,7 +1,7 @@
 """Committed golden fixtures (tests/golden/, written by tests/golden/make_golden.py
 from CPU torch running the reference's op chain) against the oracle (CPU) and
-the HIP path (GPU): packed buckets, scales, unpack, evict, plan fingerprints
-and INT8Linear, bit for bit."""
+the HIP path (GPU): packed buckets, scales, unpack, evict, apply_reuse_mask,
+plan fingerprints and INT8Linear, bit for bit."""
 
 import hashlib
 import json
@@ -23,6 +23,7 @@ KV_CASES = [("kv_f32_b1h4s24d64.npz", torch.float32, (1, 4, 24, 64)),
             ("kv_bf16_b2h3s17d48.npz", torch.bfloat16, (2, 3, 17, 48)),
             ("kv_bf16_b1h2s9d45.npz", torch.bfloat16, (1, 2, 9, 45))]
 NAMES = ("fp32", "fp16", "int8", "int4")
+REUSE_CASE = "reuse_bf16_b2h4s24p16d32.npz"
 
 
 def _load(name):
@@ -52,6 +53,30 @@ def _config1():
     drop = {(int(e // H), int(e % H)) for e in np.argsort(imp, kind="stable")[: (S * H) // 4]}
     reuse = G.gen_uniform(S * H, s["reuse"]) < 0.5
     return ref, k, v, codes, drop, reuse
+
+
+def _reuse_inputs():
+    """The reuse fixture: the reference's dict mask over every current token-head
+    (False ones included) and the previous cache's post-pack evictions."""
+    z = _load(REUSE_CASE)
+    S, H = z["codes"].shape
+    mask = {(t, h): bool(z["mask"][t, h]) for t in range(S) for h in range(H)}
+    drop = {(int(t), int(h)) for t, h in z["drop"].tolist()}
+    stats = {"applied": int(z["applied"]), "skipped_precision": int(z["skipped_precision"])}
+    return z, mask, drop, stats
+
+
+def _check_buckets(z, view, as_bytes):
+    for p in NAMES:
+        if f"{p}.k" not in z.files:
+            assert p not in view
+            continue
+        d = view[p]
+        assert [tuple(e) for e in z[f"{p}.indices"].tolist()] == list(d["indices"])
+        for key in ("k", "v", "scale_k", "scale_v"):
+            if f"{p}.{key}" in z.files:
+                np.testing.assert_array_equal(as_bytes(d[key]), z[f"{p}.{key}"].reshape(-1).view(np.uint8),
+                                              err_msg=f"{p}.{key}")
 
 
 # ------------------------------------------------------------------ oracle (CPU)
@@ -95,6 +120,50 @@ def test_oracle_matches_golden_config1():
     assert O.plan_from_codes(codes)["fingerprint"] == ref["fingerprint_no_reuse"]
     mask = {(e // H, e % H): True for e in np.nonzero(reuse)[0]}
     assert O.plan_from_codes(codes, mask)["fingerprint"] == ref["fingerprint_reuse"]
+
+
+def test_oracle_matches_golden_reuse():
+    """apply_reuse_mask from a shorter previous cache with evicted and
+    cross-precision entries: copied rows, untouched rows and both counters."""
+    z, mask, drop, stats = _reuse_inputs()
+    cur = O.kv_pack(z["k"], z["v"], O.BF16, z["codes"], 16)
+    prev = O.kv_pack(z["k_prev"], z["v_prev"], O.BF16, z["codes_prev"], 16)
+    assert O.kv_evict(prev, drop) == len(drop)
+    assert O.kv_apply_reuse_mask(cur, prev, mask) == stats
+    _check_buckets(z, cur.packed_data, lambda a: np.ascontiguousarray(a).reshape(-1).view(np.uint8))
+    uk, uv = O.kv_unpack(cur)
+    np.testing.assert_array_equal(uk.view(np.uint32), z["unpack_k"].view(np.uint32))
+    np.testing.assert_array_equal(uv.view(np.uint32), z["unpack_v"].view(np.uint32))
+
+
+def test_golden_reuse_covers_every_branch():
+    """The fixture exercises every outcome of the reference's loop
+    (packed_kv_cache.py:797-808): same-bucket copies in all four buckets,
+    cross-bucket skips, and masked entries the previous cache does not hold
+    (code 4, evicted after packing, or beyond its seq_len), which count in
+    neither counter."""
+    z, mask, drop, stats = _reuse_inputs()
+    codes, prev = z["codes"], z["codes_prev"]
+    seen = {}
+    for (t, h), on in mask.items():
+        if not on or codes[t, h] == 4:
+            continue
+        if t >= prev.shape[0]:
+            kind = "beyond"
+        elif prev[t, h] == 4:
+            kind = "prev_code4"
+        elif (t, h) in drop:
+            kind = "prev_evicted"
+        elif prev[t, h] == codes[t, h]:
+            kind = "same_" + NAMES[codes[t, h]]
+        else:
+            kind = "cross"
+        seen[kind] = seen.get(kind, 0) + 1
+    for kind in ("same_fp32", "same_fp16", "same_int8", "same_int4", "cross", "prev_code4",
+                 "prev_evicted", "beyond"):
+        assert seen.get(kind, 0) >= 1, kind
+    assert stats["applied"] == sum(v for k, v in seen.items() if k.startswith("same_"))
+    assert stats["skipped_precision"] == seen["cross"]
 
 
 def test_oracle_matches_golden_int8_linear():
@@ -162,6 +231,20 @@ def test_hip_matches_golden_config1(dev):
     assert PrecisionPlan.from_codes(dcodes).fingerprint == ref["fingerprint_no_reuse"]
     mask = {(int(e // H), int(e % H)): True for e in np.nonzero(reuse)[0]}
     assert PrecisionPlan.from_codes(dcodes, reuse_mask=mask).fingerprint == ref["fingerprint_reuse"]
+
+
+@pytest.mark.gpu
+def test_hip_matches_golden_reuse(dev):
+    z, mask, drop, stats = _reuse_inputs()
+    cur = _device_pack(_tensor(z["k"], torch.bfloat16), _tensor(z["v"], torch.bfloat16), z["codes"], dev)
+    prev = _device_pack(_tensor(z["k_prev"], torch.bfloat16), _tensor(z["v_prev"], torch.bfloat16),
+                        z["codes_prev"], dev)
+    assert prev.evict(drop) == len(drop)
+    assert cur.apply_reuse_mask(prev, mask, return_stats=True) == stats
+    _check_buckets(z, cur.packed_data, bits)
+    uk, uv = cur.unpack()
+    np.testing.assert_array_equal(to_np(uk).view(np.uint32), z["unpack_k"].view(np.uint32))
+    np.testing.assert_array_equal(to_np(uv).view(np.uint32), z["unpack_v"].view(np.uint32))
 
 
 @pytest.mark.gpu
