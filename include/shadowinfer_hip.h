@@ -67,6 +67,20 @@ int si_abi_version(void);
  * to counts[1] (both stay 0 on a correct device). */
 int si_check_bf16_convert(unsigned long long* counts, si_stream_t stream);
 
+/* Test and tuning controls, no reference counterpart. Nothing in the library
+ * reads the environment: these process-wide settings change a kernel choice
+ * only when a caller sets them explicitly (tests that compare two code paths
+ * of one operation, tile sweeps). Both start off.
+ *
+ * si_tune_gemm_plan: kind < 0 restores the automatic INT8 GEMM plan; kind >= 0
+ * forces that internal tile kind (si_gemm.hip, enum Kind) and splits > 0 the
+ * number of K splits of the tile kernels, for every later GEMM launch.
+ * si_tune_attn_offset64: on != 0 makes the packed attention use its 64-bit
+ * bucket addressing at every size (normally only caches of 2^31 bytes and
+ * more do), so the two addressing paths can be compared on small caches. */
+void si_tune_gemm_plan(int kind, int splits);
+void si_tune_attn_offset64(int on);
+
 /* Thread-local text of the last failure (empty string if none). Replaces the
  * TORCH_CHECK messages of shadowinfer/kernels/cpp/quantize_int4.cu:176-177. */
 const char* si_last_error(void);

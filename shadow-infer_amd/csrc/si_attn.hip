@@ -22,9 +22,7 @@
 // fp32 online softmax; fp16 entries of the cache are exact in fp16, int8/int4
 // values q*s are rounded once to fp16, and P is rounded to fp16 for the P.V
 // MFMAs (its row sum adds the same fp16 values).
-#include <stdlib.h>
-
-
+#include <atomic>
 #include <type_traits>
 
 #include "si_kv_common.h"
@@ -829,6 +827,9 @@ void launch_attn_o(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_
   }
 }
 
+// Set by si_tune_attn_offset64 (tests): 64-bit addressing at every size.
+std::atomic<int> g_force_offset64{0};
+
 // A bucket holds at most n_max = S_kv * H entries; fp32 rows (B * D * 4 bytes)
 // bound the byte offsets of every bucket and scale buffer.
 template <int D, int QDT>
@@ -836,10 +837,10 @@ void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t 
                  int64_t Sq, int64_t cap, const int32_t* counts, const int32_t* lists,
                  const Buckets& bk, int64_t g, float scale_log2, void* out, int odt,
                  const OutStrides& os, int64_t n_max) {
-  // SI_ATTN_OFFSET64 (any value) selects the 64-bit addressing at every size, so tests can
+  // si_tune_attn_offset64 selects the 64-bit addressing at every size, so tests can
   // compare the two paths on small caches.
   if (n_max * B * D * 4 < ((int64_t)1 << 31) && B * D < ((int64_t)1 << 21) &&
-      getenv("SI_ATTN_OFFSET64") == nullptr)
+      !g_force_offset64.load(std::memory_order_relaxed))
     launch_attn_o<D, QDT, true>(sdt, grid, st, q, B, H, Sq, cap, counts, lists, bk, g, scale_log2,
                                 out, odt, os);
   else
@@ -851,6 +852,10 @@ void launch_attn(int sdt, dim3 grid, hipStream_t st, const uint16_t* q, int64_t 
 }  // namespace si
 
 using namespace si;
+
+extern "C" void si_tune_attn_offset64(int on) {
+  g_force_offset64.store(on != 0 ? 1 : 0, std::memory_order_relaxed);
+}
 
 extern "C" size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv) {
   if (H <= 0 || S_kv <= 0) return 0;

@@ -26,8 +26,7 @@
 //
 // Split-K partial sums are int32 and are added by gemm_finalize (integer adds:
 // the result does not depend on the order).
-#include <stdlib.h>
-
+#include <atomic>
 #include <mutex>
 
 #include "si_common.h"
@@ -1116,24 +1115,12 @@ struct Plan {
   int bm, bn, bk;
 };
 
-// Tile choice override for tuning sweeps: SI_GEMM_TILE=<Kind> in the
-// environment (read once); unset = automatic choice by M.
-int forced_kind() {
-  static const int kind = [] {
-    const char* v = getenv("SI_GEMM_TILE");
-    return v != nullptr ? atoi(v) : -1;
-  }();
-  return kind;
-}
-
-// Split-K override for tuning sweeps of the tile kernels: SI_GEMM_SPLITS=<n>.
-int forced_splits() {
-  static const int splits = [] {
-    const char* v = getenv("SI_GEMM_SPLITS");
-    return v != nullptr ? atoi(v) : 0;
-  }();
-  return splits;
-}
+// Tile and split-K overrides set by si_tune_gemm_plan (tests and tile
+// sweeps); -1 / 0 = automatic choice.
+std::atomic<int> g_forced_kind{-1};
+std::atomic<int> g_forced_splits{0};
+int forced_kind() { return g_forced_kind.load(std::memory_order_relaxed); }
+int forced_splits() { return g_forced_splits.load(std::memory_order_relaxed); }
 
 // Tile and split-K choice for 16 < M <= 128 with K % 128 == 0 (and up to
 // M = 512 where the larger tiles would leave most CUs idle), where each CU
@@ -1472,6 +1459,11 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
 }  // namespace si
 
 using namespace si;
+
+extern "C" void si_tune_gemm_plan(int kind, int splits) {
+  g_forced_kind.store(kind < 0 ? -1 : kind, std::memory_order_relaxed);
+  g_forced_splits.store(splits > 0 ? splits : 0, std::memory_order_relaxed);
+}
 
 extern "C" size_t si_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;

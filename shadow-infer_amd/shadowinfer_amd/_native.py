@@ -42,6 +42,8 @@ _SIGNATURES = {
     "si_abi_version": (_i32, []),
     "si_last_error": (ctypes.c_char_p, []),
     "si_check_bf16_convert": (_i32, [_vp, _vp]),
+    "si_tune_gemm_plan": (None, [_i32, _i32]),
+    "si_tune_attn_offset64": (None, [_i32]),
     "si_plan_workspace_bytes": (_sz, [_i64]),
     "si_plan_scan": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "si_plan_scatter": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),

@@ -12,6 +12,7 @@ import torch
 
 from helpers import kv_inputs, mixed_codes, oracle_pack
 from oracle import oracle as O
+from shadowinfer_amd import _native
 from shadowinfer_amd.shadowkv import PackedKVCache, PrecisionPlan, packed_attention
 
 pytestmark = pytest.mark.gpu
@@ -147,10 +148,10 @@ def test_attention_entry_points_agree(dev, D):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("D", [64, 128])
-def test_attention_offset_widths_agree(dev, D, monkeypatch):
+def test_attention_offset_widths_agree(dev, D):
     """Caches below 2^31 bytes address bucket rows with 32-bit offsets; larger
-    ones with 64-bit addresses. SI_ATTN_OFFSET64 selects the 64-bit path at any
-    size: both give the same bits, and both match the oracle."""
+    ones with 64-bit addresses. si_tune_attn_offset64 selects the 64-bit path at
+    any size: both give the same bits, and both match the oracle."""
     B, H, S = 2, 3, 300
     k, v = kv_inputs(B, H, S, D, torch.bfloat16, seed=D + 7, outlier_frac=0.02)
     codes = mixed_codes(S, H, seed=D + 7, probs=(1, 1, 2, 1), sink=4, evicted=0.05)
@@ -158,9 +159,12 @@ def test_attention_offset_widths_agree(dev, D, monkeypatch):
     g = torch.Generator().manual_seed(D)
     q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
     narrow = packed_attention(q, cache)
-    monkeypatch.setenv("SI_ATTN_OFFSET64", "1")
-    wide = packed_attention(q, cache)
-    monkeypatch.delenv("SI_ATTN_OFFSET64")
+    lib = _native.load()
+    lib.si_tune_attn_offset64(1)
+    try:
+        wide = packed_attention(q, cache)
+    finally:
+        lib.si_tune_attn_offset64(0)
     assert torch.equal(narrow, wide)
     rk, rv = O.kv_unpack(oracle_pack(k, v, codes))
     ref = O.attention(q.float().cpu().numpy().reshape(B * H, S, D), rk.reshape(B * H, S, D),
