@@ -11,11 +11,14 @@
  *   an item marks entry t * H + h when it is a 2-tuple equal to (t, h) with
  *   0 <= t < S and 0 <= h < H (for a dict, when its value is also truthy).
  *
- * Elements that are ints (bool included), objects with __index__ (numpy
- * integers) or floats with an integral value compare equal to that integer,
- * as in Python. Items that are not 2-tuples can never equal a (t, h) tuple and
- * are skipped. Any other element type makes the call return None, and the
- * caller then decides item by item in Python.
+ * Elements that are ints (bool included), numpy bools, objects with
+ * __index__ (numpy integers) or floats with an integral value compare equal to
+ * that integer, as in Python. Items that are not 2-tuples can never equal a
+ * (t, h) tuple and are skipped. A dict value's truthiness is evaluated only
+ * for keys that are in-range pairs, as the reference evaluates
+ * reuse_mask.get(entry) only for entries of the cache. Any other element
+ * type, or a value whose truthiness raises, makes the call return None, and
+ * the caller then decides item by item in Python.
  *
  * token_head_mask(items, S, H, out, is_dict) -> int (entries marked, counting
  * repeats) or None. `out` is a writable buffer of at least S * H bytes; it is
@@ -25,10 +28,24 @@
 #include <Python.h>
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
+
+/* numpy's bool scalar: equal to 0 or 1, but its __index__ is deprecated
+ * (a DeprecationWarning, an error under -W error), so it is read by value. */
+static int is_numpy_bool(PyObject* o) {
+  const char* n = Py_TYPE(o)->tp_name;
+  return strcmp(n, "numpy.bool") == 0 || strcmp(n, "numpy.bool_") == 0;
+}
 
 /* 1: integral value in *out; 0: never equal to an in-range integer;
  * -1: undecided (unknown type); -2: Python error set. */
 static int element_index(PyObject* o, long long* out) {
+  if (is_numpy_bool(o)) {
+    const int b = PyObject_IsTrue(o);
+    if (b < 0) return -2;
+    *out = b;
+    return 1;
+  }
   if (PyLong_Check(o)) {
     int overflow = 0;
     long long v = PyLong_AsLongLongAndOverflow(o, &overflow);
@@ -57,8 +74,9 @@ static int element_index(PyObject* o, long long* out) {
   return -1;
 }
 
-/* 1 marked, 0 not marked, -1 undecided, -2 error */
-static int mark_item(PyObject* item, long long S, long long H, unsigned char* out) {
+/* 1: item equals the in-range pair (t, h), *entry = t * H + h; 0: it equals
+ * no in-range pair; -1 undecided; -2 error. Writes nothing. */
+static int item_entry(PyObject* item, long long S, long long H, long long* entry) {
   if (!PyTuple_Check(item) || PyTuple_GET_SIZE(item) != 2) return 0;
   long long t = 0, h = 0;
   int rt = element_index(PyTuple_GET_ITEM(item, 0), &t);
@@ -67,7 +85,7 @@ static int mark_item(PyObject* item, long long S, long long H, unsigned char* ou
   if (rh < 0) return rh;
   if (rt == 0 || rh == 0) return 0;
   if (t < 0 || t >= S || h < 0 || h >= H) return 0;
-  out[t * H + h] = 1;
+  *entry = t * H + h;
   return 1;
 }
 
@@ -95,13 +113,8 @@ static PyObject* token_head_mask(PyObject* self, PyObject* args) {
     Py_ssize_t pos = 0;
     PyObject *key, *value;
     while (PyDict_Next(items, &pos, &key, &value)) {
-      const int truthy = PyObject_IsTrue(value);
-      if (truthy < 0) {
-        PyBuffer_Release(&buf);
-        return NULL;
-      }
-      if (!truthy) continue;
-      const int r = mark_item(key, S, H, out);
+      long long e = 0;
+      const int r = item_entry(key, S, H, &e);
       if (r == -2) {
         PyBuffer_Release(&buf);
         return NULL;
@@ -110,7 +123,16 @@ static PyObject* token_head_mask(PyObject* self, PyObject* args) {
         undecided = 1;
         break;
       }
-      marked += r;
+      if (r == 0) continue;
+      const int truthy = PyObject_IsTrue(value);
+      if (truthy < 0) { /* decided by the Python rule, which raises the same error */
+        PyErr_Clear();
+        undecided = 1;
+        break;
+      }
+      if (!truthy) continue;
+      out[e] = 1;
+      marked += 1;
     }
   } else {
     PyObject* it = PyObject_GetIter(items);
@@ -120,8 +142,10 @@ static PyObject* token_head_mask(PyObject* self, PyObject* args) {
     }
     PyObject* item;
     while ((item = PyIter_Next(it)) != NULL) {
-      const int r = mark_item(item, S, H, out);
+      long long e = 0;
+      const int r = item_entry(item, S, H, &e);
       Py_DECREF(item);
+      if (r == 1) out[e] = 1;
       if (r == -2) {
         Py_DECREF(it);
         PyBuffer_Release(&buf);

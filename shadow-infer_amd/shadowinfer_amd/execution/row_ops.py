@@ -11,6 +11,7 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _native
+from .._checks import check_rope_args as _check_rope_args
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -53,16 +54,6 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, want_y: bool = Tr
             (None if xo is None else xo.view(x.shape)))
 
 
-def _check_rope_args(qkv, cos, sin, batch, seq, heads, head_dim, what):
-    _native.require_device(qkv, what)
-    if qkv.shape != (batch * seq, 3 * heads * head_dim):
-        raise ValueError(f"qkv must be [{batch * seq}, {3 * heads * head_dim}], got {tuple(qkv.shape)}")
-    if cos.shape != (seq, head_dim) or sin.shape != (seq, head_dim):
-        raise ValueError(f"cos/sin must be [{seq}, {head_dim}]")
-    if cos.dtype != qkv.dtype or sin.dtype != qkv.dtype:
-        raise ValueError("cos/sin must have qkv's dtype")
-
-
 def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, batch: int, seq: int,
                heads: int, head_dim: int, kv: bool = True
                ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
@@ -70,12 +61,13 @@ def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, batch: i
     (models/diffusion_llama.py:362-373); ``cos``/``sin`` ``[S, D]`` in qkv's dtype.
     ``kv=False`` writes q only (k and v are returned as None)."""
     _check_rope_args(qkv, cos, sin, batch, seq, heads, head_dim, "rope_split")
-    src = qkv.contiguous()
+    # contiguous copies stay bound until the launch is queued
+    src, cos_c, sin_c = qkv.contiguous(), cos.contiguous(), sin.contiguous()
     q = torch.empty(batch, heads, seq, head_dim, dtype=qkv.dtype, device=qkv.device)
     k = torch.empty_like(q) if kv else None
     v = torch.empty_like(q) if kv else None
     _native.call("si_rope_split", src.data_ptr(), _native.dtype_code(qkv.dtype), batch, seq,
-                 heads, head_dim, cos.contiguous().data_ptr(), sin.contiguous().data_ptr(),
+                 heads, head_dim, cos_c.data_ptr(), sin_c.data_ptr(),
                  q.data_ptr(), _native.ptr(k), _native.ptr(v), _native.stream(qkv.device))
     return q, k, v
 

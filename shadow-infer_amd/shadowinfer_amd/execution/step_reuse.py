@@ -23,10 +23,12 @@ How it runs here:
   so a gated layer costs one small device read;
 * the reused output is one HIP pass (``si_reuse_apply``) instead of a
   subtraction and an addition over the whole hidden state;
-* ``threshold=inf`` accepts every layer that has a record of the right shape
-  without computing the drift: no device read at all, and a denoising loop
-  stays asynchronous; ``reusable_layers`` limits reuse to a fixed set of
-  layers (e.g. every other block).
+* ``threshold=inf`` keeps the reference's outcome: the drift is still
+  computed and logged, a record with an all-zero input is dropped and a NaN
+  drift refuses reuse. ``skip_drift=True`` (no reference counterpart) accepts
+  every record of the right shape without computing the drift: no device
+  read at all, so a denoising loop stays asynchronous; ``reusable_layers``
+  limits reuse to a fixed set of layers (e.g. every other block).
 """
 
 from __future__ import annotations
@@ -35,6 +37,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Any, Dict, FrozenSet, List, Optional
 
+import numpy as np
 import torch
 
 from .. import _native
@@ -43,12 +46,16 @@ from .. import _native
 @dataclass(frozen=True)
 class StepReuseConfig:
     """The reference's knobs (``enabled``, ``threshold``, ``warmup_steps``)
-    plus ``reusable_layers`` (None: every layer may be reused)."""
+    plus ``reusable_layers`` (None: every layer may be reused) and
+    ``skip_drift`` (reuse every record of the right shape without computing
+    the drift; the gate then neither drops all-zero records nor refuses NaN
+    drifts, and ``stats()['drifts']`` stays empty)."""
 
     enabled: bool = False
     threshold: float = 0.1
     warmup_steps: int = 1
     reusable_layers: Optional[FrozenSet[int]] = None
+    skip_drift: bool = False
 
     def __post_init__(self) -> None:
         if self.threshold < 0:
@@ -80,9 +87,16 @@ class _StepLog:
     drifts: Dict[int, float] = field(default_factory=dict)
 
 
-def _round_to(x: float, dtype: torch.dtype) -> float:
-    """An fp32 value rounded to ``dtype`` (round to nearest even), as float."""
-    return float(torch.tensor(x, dtype=torch.float32).to(dtype).float())
+def _round_to(x: np.float32, dtype: torch.dtype) -> np.float32:
+    """An fp32 value rounded to ``dtype`` (round to nearest even)."""
+    return np.float32(torch.tensor(float(x), dtype=torch.float32).to(dtype).float().item())
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """``t`` contiguous at a 16-byte aligned address (the reuse kernels read
+    16 bytes per lane); a view at an odd offset is copied."""
+    c = t.contiguous()
+    return c if c.data_ptr() % 16 == 0 else c.clone(memory_format=torch.contiguous_format)
 
 
 class StepReuseState:
@@ -106,8 +120,8 @@ class StepReuseState:
         arithmetic; None when ``hidden_in`` is all zeros (a NaN drift, from
         non-finite states, never passes the gate)."""
         _native.require_device(hidden, "StepReuseState.relative_drift")
-        a = hidden.contiguous()
-        b = record.hidden_in.contiguous()
+        a = _aligned(hidden)
+        b = _aligned(record.hidden_in)
         dev = a.device
         ws_bytes = _native.size_query("si_reuse_drift_workspace_bytes", a.numel())
         buf = self._scratch.get(dev)
@@ -117,12 +131,15 @@ class StepReuseState:
         sums = buf[ws_bytes:ws_bytes + 8].view(torch.float32)
         _native.call("si_reuse_drift", a.data_ptr(), b.data_ptr(), _native.dtype_code(a.dtype),
                      a.numel(), sums.data_ptr(), buf.data_ptr(), ws_bytes, _native.stream(dev))
-        s_diff, s_in = (float(x) for x in sums.cpu().tolist())
+        s_diff, s_in = sums.cpu().numpy()
         dt = a.dtype
-        denom = _round_to(math.sqrt(s_in), dt) if s_in >= 0.0 else float("nan")
-        if denom <= 0.0:
-            return None
-        return _round_to(_round_to(math.sqrt(s_diff), dt) / denom, dt)
+        # torch: each norm is the fp32 square root of the fp32 sum, rounded to
+        # the dtype; the quotient is taken in fp32 and rounded to the dtype
+        with np.errstate(invalid="ignore", divide="ignore"):
+            denom = _round_to(np.sqrt(s_in), dt)
+            if denom <= 0.0:
+                return None
+            return float(_round_to(_round_to(np.sqrt(s_diff), dt) / denom, dt))
 
     def gate(self, layer: int, hidden: torch.Tensor, step_id: int,
              config: StepReuseConfig) -> Optional[LayerRecord]:
@@ -133,7 +150,7 @@ class StepReuseState:
         if record is None or record.hidden_in.shape != hidden.shape:
             self.records.pop(layer, None)
             return None
-        if math.isinf(config.threshold):
+        if config.skip_drift:
             return record
         drift = self.relative_drift(record, hidden)
         if drift is None:
@@ -146,9 +163,9 @@ class StepReuseState:
     def reuse(self, layer: int, record: LayerRecord, hidden: torch.Tensor) -> torch.Tensor:
         """The reused layer's output ``hidden_out + (hidden - hidden_in)``."""
         _native.require_device(hidden, "StepReuseState.reuse")
-        h = hidden.contiguous()
-        hin = record.hidden_in.contiguous()
-        hout = record.hidden_out.contiguous()
+        h = _aligned(hidden)
+        hin = _aligned(record.hidden_in)
+        hout = _aligned(record.hidden_out)
         out = torch.empty_like(h)
         _native.call("si_reuse_apply", h.data_ptr(), hin.data_ptr(), hout.data_ptr(),
                      _native.dtype_code(h.dtype), h.numel(), out.data_ptr(),

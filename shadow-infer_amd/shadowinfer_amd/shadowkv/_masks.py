@@ -49,20 +49,29 @@ def _ext():
     return _mod
 
 
+def _entry(item, S: int, H: int) -> Optional[int]:
+    """``t * H + h`` when ``item`` equals the in-range pair ``(t, h)`` (Python's
+    own tuple equality: 3.0 matches 3, 3.5 and "3" match nothing), else None."""
+    if not isinstance(item, tuple) or len(item) != 2:
+        return None
+    try:
+        t, h = int(item[0]), int(item[1])
+    except (TypeError, ValueError, OverflowError):
+        return None
+    if (t, h) == item and 0 <= t < S and 0 <= h < H:
+        return t * H + h
+    return None
+
+
 def _mark_python(items, S: int, H: int, out: np.ndarray, is_dict: bool) -> int:
-    """Item by item: ``(int(t), int(h)) == item`` is Python's own equality of
-    the item with an integer pair (3.0 matches 3, 3.5 matches nothing)."""
+    """Item by item; a dict value's truthiness is evaluated only for in-range
+    pairs (the reference evaluates ``reuse_mask.get(entry)`` only for entries
+    of the cache, packed_kv_cache.py:797-799)."""
     marked = 0
-    it = compress(items.keys(), items.values()) if is_dict else items
-    for item in it:
-        if not isinstance(item, tuple) or len(item) != 2:
-            continue
-        try:
-            t, h = int(item[0]), int(item[1])
-        except (TypeError, ValueError, OverflowError):
-            continue
-        if (t, h) == item and 0 <= t < S and 0 <= h < H:
-            out[t * H + h] = 1
+    for item, value in (items.items() if is_dict else ((i, True) for i in items)):
+        e = _entry(item, S, H)
+        if e is not None and value:
+            out[e] = 1
             marked += 1
     return marked
 

@@ -28,6 +28,7 @@ import numpy as np
 import torch
 
 from .. import _native
+from .._checks import check_rope_args as _check_rope_args
 from ._masks import token_head_mask
 from .precision_plan import EVICTED, PRECISION_ORDER, DeviceGrouping, PrecisionPlan
 
@@ -77,14 +78,13 @@ class PackedKVCache:
         rotate-half tables ``cos``/``sin`` ``[S, D]`` (si_kv_pack_rope_flat): the
         dense K/V are never written. bf16/fp16, D = 64 or 128."""
         B, S, H, D = batch_size, seq_len, num_heads, head_dim
-        if qkv.shape != (B * S, 3 * H * D):
-            raise ValueError(f"qkv must be [{B * S}, {3 * H * D}], got {tuple(qkv.shape)}")
+        # qkv [B*S, 3*H*D] on a GPU, cos/sin [S, D] in its dtype and on its device
+        _check_rope_args(qkv, cos, sin, B, S, H, D, "PackedKVCache.pack_projection")
         if plan.seq_len != S or plan.num_heads != H:
             raise ValueError(
                 "PrecisionPlan shape mismatch: plan "
                 f"(seq_len={plan.seq_len}, num_heads={plan.num_heads}) vs "
                 f"tensor (seq_len={S}, num_heads={H})")
-        _native.require_device(qkv, "PackedKVCache.pack_projection")
         dev = qkv.device
         cache = cls(B, H, S, D, device=dev)
         grouping = plan.device_grouping()
@@ -99,8 +99,9 @@ class PackedKVCache:
         cache._view = None
         flat = grouping.flat_lists(S, H)
         counts = (ctypes.c_int64 * 5)(*[int(c) for c in grouping.counts])
-        _native.call("si_kv_pack_rope_flat", qkv.contiguous().data_ptr(),
-                     cos.contiguous().data_ptr(), sin.contiguous().data_ptr(),
+        # contiguous copies stay bound until the launch is queued
+        src, cos_c, sin_c = qkv.contiguous(), cos.contiguous(), sin.contiguous()
+        _native.call("si_kv_pack_rope_flat", src.data_ptr(), cos_c.data_ptr(), sin_c.data_ptr(),
                      _native.dtype_code(qkv.dtype), B, H, S, D, g, grouping.code.data_ptr(),
                      grouping.slot.data_ptr(), _native.table4([f.data_ptr() for f in flat]),
                      counts, cache._bucket_table(), _native.stream(dev))

@@ -657,6 +657,51 @@ def test_reuse_kernels_match_the_torch_ops(dev, dtype, n):
 
 
 @pytest.mark.gpu
+def test_reuse_gate_with_infinite_threshold_keeps_the_reference_outcome(dev):
+    """threshold=inf still computes the drift (execution/step_reuse.py:71-95):
+    an all-zero recorded input drops the record and recomputes, a NaN drift
+    refuses reuse, a finite one is logged and reused. skip_drift=True reuses
+    every record of the right shape without reading the device."""
+    from shadowinfer_amd.execution import StepReuseConfig, StepReuseState
+    from shadowinfer_amd.execution.step_reuse import LayerRecord
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(2, 8, 64, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.randn(2, 8, 64, generator=g).to(torch.bfloat16).to(dev)
+    inf = StepReuseConfig(enabled=True, threshold=float("inf"), warmup_steps=0)
+    st = StepReuseState()
+    st.records[0] = LayerRecord(torch.zeros_like(h), out)
+    assert st.gate(0, h, 1, inf) is None and 0 not in st.records
+    nan_h = h.clone()
+    nan_h[0, 0, 0] = float("nan")
+    st.records[0] = LayerRecord(h, out)
+    assert st.gate(0, nan_h, 1, inf) is None and 0 in st.records
+    assert math.isnan(st.stats()["drifts"][0])
+    st.new_step()
+    assert st.gate(0, h * 1.5, 1, inf) is st.records[0]
+    assert st.stats()["drifts"][0] == pytest.approx(0.5, rel=2 ** -7)
+    skip = StepReuseConfig(enabled=True, threshold=float("inf"), warmup_steps=0, skip_drift=True)
+    st = StepReuseState()
+    st.records[0] = LayerRecord(torch.zeros_like(h), out)
+    assert st.gate(0, h, 1, skip) is st.records[0] and st.stats()["drifts"] == {}
+
+
+@pytest.mark.gpu
+def test_reuse_kernels_take_views_at_any_offset(dev):
+    """A hidden state that is a view at an odd element offset (not 16-byte
+    aligned) works like its contiguous copy in the drift and the reused output."""
+    from shadowinfer_amd.execution import StepReuseState
+    from shadowinfer_amd.execution.step_reuse import LayerRecord
+    g = torch.Generator().manual_seed(6)
+    base = torch.randn(3, 4104, generator=g).to(torch.bfloat16).to(dev)
+    h, hin, hout = base[0, 1:4097], base[1, 3:4099], base[2, 5:4101]
+    st = StepReuseState()
+    rec = LayerRecord(hin, hout)
+    got = st.reuse(0, rec, h)
+    assert torch.equal(got, hout + (h - hin))
+    assert st.relative_drift(rec, h) == st.relative_drift(LayerRecord(hin.clone(), hout), h.clone())
+
+
+@pytest.mark.gpu
 def test_denoise_loop_progress(dev):
     from shadowinfer_amd.execution import StepReuseConfig, StepReuseState, mask_tokens
     m = _model(dev)

@@ -198,6 +198,24 @@ def test_cpu_tensors_fail_loudly():
         INT8Linear.from_linear(nn.Linear(8, 8))
 
 
+def test_rope_pack_rejects_bad_tables_before_any_launch():
+    """pack_projection reads cos/sin [S, D] in qkv's dtype for every token: a
+    short table or one of another dtype is a ValueError (a short table would be
+    read past its end, an fp32 one as bf16 pairs); well-formed CPU tensors are
+    the usual no-CPU-implementation error."""
+    B, S, H, D = 1, 6, 2, 64
+    plan = PrecisionPlan.from_codes(torch.full((S, H), 2, dtype=torch.int8))
+    qkv = torch.zeros(B * S, 3 * H * D, dtype=torch.bfloat16)
+    good = torch.zeros(S, D, dtype=torch.bfloat16)
+    for cos, sin in ((good[: S - 1], good[: S - 1]), (good.float(), good.float()), (good, good[:, :32])):
+        with pytest.raises(ValueError, match="cos/sin"):
+            PackedKVCache.pack_projection(qkv, cos, sin, B, S, H, D, 16, plan)
+    with pytest.raises(ValueError, match="qkv must be"):
+        PackedKVCache.pack_projection(qkv[:, : 2 * H * D], good, good, B, S, H, D, 16, plan)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        PackedKVCache.pack_projection(qkv, good, good, B, S, H, D, 16, plan)
+
+
 def test_empty_cache_is_safe_without_device():
     """reference tests/test_kv_store.py:528-552 (UT-12.10)."""
     packed = PackedKVCache(1, 2, 8, 64)
@@ -342,6 +360,39 @@ def test_token_head_masks_follow_python_membership():
         _masks._mark_python(container, S, H, slow, is_dict)
         np.testing.assert_array_equal(slow, want)
     assert _masks.token_head_mask(set(), S, H) is None
+
+
+def test_token_head_masks_evaluate_values_only_for_pairs(recwarn):
+    """A dict value's truthiness is evaluated only for keys that are in-range
+    (t, h) pairs: a value whose __bool__ raises under an irrelevant key is never
+    touched (the reference looks values up only for entries of the cache). Under
+    a relevant key it raises, as ``if reuse_mask.get(entry)`` would. numpy bool
+    elements equal 0 / 1, as in Python, and raise no DeprecationWarning."""
+    import warnings
+
+    import numpy as np
+    from shadowinfer_amd.shadowkv import _masks
+
+    class Boom:
+        def __bool__(self):
+            raise RuntimeError("truthiness evaluated")
+
+    S, H = 4, 2
+    d = {(1, 1): True, (9, 0): Boom(), ("x", 0): Boom(), (0, 5): Boom(), (2,): Boom(),
+         (np.True_, np.False_): 1, (np.int64(3), np.bool_(True)): np.True_}
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        got = _masks.token_head_mask(d, S, H, is_dict=True)
+        slow = np.zeros(S * H, np.uint8)
+        _masks._mark_python(d, S, H, slow, True)
+        s = _masks.token_head_mask({(np.True_, np.True_), (np.bool_(False), 1)}, S, H)
+    want = np.zeros(S * H, np.uint8)
+    want[[1 * H + 1, 1 * H + 0, 3 * H + 1]] = 1
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(slow, want)
+    np.testing.assert_array_equal(np.nonzero(s)[0], [0 * H + 1, 1 * H + 1])
+    with pytest.raises(RuntimeError, match="truthiness"):
+        _masks.token_head_mask({(0, 0): Boom()}, S, H, is_dict=True)
 
 
 def test_map_to_codes_random_maps_match_the_dense_rule():
