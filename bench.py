@@ -385,16 +385,18 @@ def bench_kv(torch, dev, steps, warmup):
     new_counts = [int(c) for c in n_cnt.tolist()]
     fresh = cur._alloc_buckets(new_counts, dev, torch.bfloat16)
     ftable = cur._bucket_table(fresh)
-    n_flat = [torch.empty(new_counts[p], dtype=torch.long, device=dev) for p in range(4)]
+    # PackedKVCache.evict's lists: allocated at the old bucket sizes (which
+    # bound the new ones) before the fused rescan fills them
+    old_counts = [int(c) for c in L0["plan"].device_grouping().counts[:4]]
+    n_flat = [torch.empty(c, dtype=torch.long, device=dev) for c in old_counts]
     n_flat_t = _native.table4([f.data_ptr() for f in n_flat])
+    n_cap = (ctypes.c_int64 * 4)(*old_counts)
     n_counts = (ctypes.c_int64 * 5)(*new_counts)
-    none4 = _native.table4([None] * 4)
 
-    def evict():  # the device work of PackedKVCache.evict: rescan, new lists, compaction
-        _native.call("si_plan_scan", L0["code"].data_ptr(), ev_u8.data_ptr(), S * H,
-                     n_code.data_ptr(), n_slot.data_ptr(), n_cnt.data_ptr(), ws.data_ptr(), ws_b, sptr)
-        _native.call("si_plan_scatter", n_code.data_ptr(), n_slot.data_ptr(), S, H, n_flat_t,
-                     none4, sptr)
+    def evict():  # the device work of PackedKVCache.evict: fused rescan + lists, compaction
+        _native.call("si_plan_scan_lists", L0["code"].data_ptr(), ev_u8.data_ptr(), S, H,
+                     n_code.data_ptr(), n_slot.data_ptr(), n_cnt.data_ptr(), n_flat_t, n_cap,
+                     ws.data_ptr(), ws_b, sptr)
         _native.call("si_kv_compact_flat", L0["slot"].data_ptr(), L0["table"], n_flat_t, n_counts,
                      ftable, S, H, B, D, GROUP, L0["sdt"], sptr)
 

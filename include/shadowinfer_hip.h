@@ -113,6 +113,19 @@ int si_plan_scatter(const int8_t* code, const int32_t* slot, int64_t S, int64_t 
                     int64_t* const* flat_out, int32_t* const* entry_out,
                     si_stream_t stream);
 
+/* si_plan_scan and si_plan_scatter in one pass over S*H entries (one
+ * counting launch and one launch that scans and fills the lists), for the
+ * rescan of PackedKVCache.evict (shadowinfer/shadowkv/packed_kv_cache.py:
+ * 679-737), whose new buckets are not known before the scan.
+ * flat_out: HOST array of 4 device int64 lists; flat_capacity: HOST int64[4],
+ * the rows each list holds (an evict passes the old bucket sizes, which bound
+ * the new ones); slots at or past a list's capacity are not written.
+ * Workspace: si_plan_workspace_bytes(S * H). */
+int si_plan_scan_lists(const int8_t* codes, const uint8_t* evict_mask, int64_t S, int64_t H,
+                       int8_t* out_code, int32_t* out_slot, int64_t* out_counts,
+                       int64_t* const* flat_out, const int64_t* flat_capacity, void* workspace,
+                       size_t workspace_bytes, si_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Packed KV cache                                                         */
 /* ---------------------------------------------------------------------- */

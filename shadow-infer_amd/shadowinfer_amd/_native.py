@@ -47,6 +47,7 @@ _SIGNATURES = {
     "si_plan_workspace_bytes": (_sz, [_i64]),
     "si_plan_scan": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "si_plan_scatter": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "si_plan_scan_lists": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "si_kv_pack": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "si_kv_pack_flat": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                _vp, _vp]),

@@ -349,7 +349,7 @@ class PackedKVCache:
                 return 0
         old = self._grouping
         dev = old.code.device
-        new = DeviceGrouping.scan(old.code, evict_mask=mask.to(dev))
+        new = old.rescan(mask.to(dev), self.seq_len, self.num_heads)
         removed = int(sum(old.counts[:4]) - sum(new.counts[:4]))
         if removed == 0:
             return 0

@@ -16,6 +16,8 @@ pack (``PackedKVCache.pack`` raises ValueError, as the reference does).
 
 from __future__ import annotations
 
+import ctypes
+
 import hashlib
 import struct
 from itertools import chain
@@ -173,6 +175,27 @@ class DeviceGrouping:
                      _native.ptr(evict_mask), n, code.data_ptr(), slot.data_ptr(),
                      counts.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream(dev))
         return DeviceGrouping(code, slot, [int(c) for c in counts.tolist()])
+
+    def rescan(self, evict_mask: torch.Tensor, S: int, H: int) -> "DeviceGrouping":
+        """The grouping without the entries ``evict_mask`` marks, flat lists
+        included, in one fused pass (si_plan_scan_lists). The lists are
+        allocated at this grouping's bucket sizes, which bound the new ones,
+        and returned as views of the new sizes."""
+        dev = self.code.device
+        n = S * H
+        ws_bytes = _native.size_query("si_plan_workspace_bytes", n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        code = torch.empty(n, dtype=torch.int8, device=dev)
+        slot = torch.empty(n, dtype=torch.int32, device=dev)
+        counts = torch.empty(5, dtype=torch.int64, device=dev)
+        cap = [int(c) for c in self.counts[:4]]
+        full = [torch.empty(c, dtype=torch.long, device=dev) for c in cap]
+        _native.call("si_plan_scan_lists", self.code.data_ptr(), evict_mask.data_ptr(), S, H,
+                     code.data_ptr(), slot.data_ptr(), counts.data_ptr(),
+                     _native.table4([f.data_ptr() for f in full]), (ctypes.c_int64 * 4)(*cap),
+                     ws.data_ptr(), ws_bytes, _native.stream(dev))
+        new_counts = [int(c) for c in counts.tolist()]
+        return DeviceGrouping(code, slot, new_counts, [f[:c] for f, c in zip(full, new_counts)])
 
 
 class PrecisionPlan:
