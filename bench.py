@@ -494,10 +494,19 @@ def bench_gemm(torch, dev, iters=50):
                          w.data_ptr(), sw.data_ptr(), None, y.data_ptr(), lws.data_ptr(), lws_b,
                          sptr)
 
+        def gemm_dequant():  # the GEMM with INT8Linear's epilogue, bf16 out
+            w = ws[it[0] % copies]
+            it[0] += 1
+            _native.call("si_gemm_i8_dequant", q.data_ptr(), sx.data_ptr(), w.data_ptr(),
+                         sw.data_ptr(), None, M, N, K, y.data_ptr(), _native.DT_BF16,
+                         gws.data_ptr(), gws_b, sptr)
+
         for _ in range(5):
             gemm()
             forward()
+            gemm_dequant()
         ms_gemm = timer.time(gemm, iters)
+        ms_deq = timer.time(gemm_dequant, iters)
         ms_fwd = timer.time(forward, iters)
         ops = 2.0 * M * K * N
         # The vendor library on the same operands: hipBLASLt through
@@ -517,6 +526,8 @@ def bench_gemm(torch, dev, iters=50):
             "gemm_tops": ops / (ms_gemm * 1e-3) / 1e12,
             "gemm_frac": ops / (ms_gemm * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "gemm_weight_gbs": K * N / (ms_gemm * 1e-3) / 1e9,
+            "gemm_dequant_us": ms_deq * 1e3,
+            "gemm_dequant_frac": ops / (ms_deq * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "forward_us": ms_fwd * 1e3,
             "forward_tops": ops / (ms_fwd * 1e-3) / 1e12,
         }

@@ -43,6 +43,45 @@ def test_plan_from_codes_matches_oracle(dev, S, H):
     assert plan.fingerprint == ref["fingerprint"]
 
 
+@pytest.mark.parametrize("S,H", [(1, 1), (7, 3), (1000, 3), (8192, 32), (40000, 32)])
+def test_plan_scan_lists_matches_scan_then_scatter(dev, S, H):
+    """The evict rescan with its flat lists in one pass (si_plan_scan_lists)
+    gives the code / slot / counts of si_plan_scan and the lists of
+    si_plan_scatter, on the fused path and (40000 x 32: above 2^20 entries)
+    on the three-pass fallback; no list is written at or past its capacity."""
+    from shadowinfer_amd import _native
+    import ctypes
+    rng = np.random.default_rng(S + H)
+    codes = torch.from_numpy(rng.integers(-1, 6, size=S * H).astype(np.int8)).to(dev)
+    mask = torch.from_numpy((rng.random(S * H) < 0.3).astype(np.uint8)).to(dev)
+    n = S * H
+    sp = _native.stream(dev)
+    ws_b = _native.size_query("si_plan_workspace_bytes", n)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device=dev)
+    code0 = torch.empty(n, dtype=torch.int8, device=dev)
+    slot0 = torch.empty(n, dtype=torch.int32, device=dev)
+    cnt0 = torch.empty(5, dtype=torch.int64, device=dev)
+    _native.call("si_plan_scan", codes.data_ptr(), mask.data_ptr(), n, code0.data_ptr(),
+                 slot0.data_ptr(), cnt0.data_ptr(), ws.data_ptr(), ws_b, sp)
+    counts = [int(c) for c in cnt0.tolist()]
+    ref = [torch.empty(counts[p], dtype=torch.long, device=dev) for p in range(4)]
+    _native.call("si_plan_scatter", code0.data_ptr(), slot0.data_ptr(), S, H,
+                 _native.table4([r.data_ptr() for r in ref]), _native.table4([None] * 4), sp)
+    # lists one row short of the new sizes, inside buffers with a sentinel tail
+    cap = [max(c - 1, 0) for c in counts[:4]]
+    bufs = [torch.full((c + 8,), -7, dtype=torch.long, device=dev) for c in cap]
+    code1 = torch.empty_like(code0)
+    slot1 = torch.empty_like(slot0)
+    cnt1 = torch.empty_like(cnt0)
+    _native.call("si_plan_scan_lists", codes.data_ptr(), mask.data_ptr(), S, H, code1.data_ptr(),
+                 slot1.data_ptr(), cnt1.data_ptr(), _native.table4([b.data_ptr() for b in bufs]),
+                 (ctypes.c_int64 * 4)(*cap), ws.data_ptr(), ws_b, sp)
+    assert torch.equal(code1, code0) and torch.equal(slot1, slot0) and torch.equal(cnt1, cnt0)
+    for p in range(4):
+        assert torch.equal(bufs[p][: cap[p]], ref[p][: cap[p]])
+        assert bool((bufs[p][cap[p]:] == -7).all())
+
+
 def test_plan_device_matches_host_plan(dev):
     codes = mixed_codes(300, 5, seed=3, probs=(1, 1, 1, 1), evicted=0.1)
     gpu = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
