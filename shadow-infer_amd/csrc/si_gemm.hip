@@ -5,17 +5,21 @@
 // (nn.Linear's layout). Both are K-contiguous, which is the register layout
 // of MFMA fragments, so tiles move as 16-byte chunks with no transposition.
 //
-// Three kernels:
-//  * gemm_dma (the default for M > 16): BM x BN x BK tiles copied global ->
-//    LDS by global_load_lds_dwordx4 into 4 LDS stages (no register staging,
-//    two k-tiles in flight behind the one being multiplied), XOR-swizzled
-//    16-byte chunks, v_mfma_i32_32x32x32_i8 on a 2x2 wave grid.
-//  * gemm_tile: the same tiling with register-staged copies into
-//    double-buffered, padded LDS; used where K is not a multiple of 64.
-//  * gemm_skinny (M <= 16): weight streaming. No LDS: every lane loads its
-//    v_mfma_i32_16x16x64_i8 fragments directly (16 bytes of one weight row,
-//    16 bytes of one activation row from L2); K is split so that enough
-//    wavefronts stream the weight to keep HBM busy.
+// Kernels (choose() picks one per shape):
+//  * gemm_dma (M > 32, and M > 16 outside gemm_rows' widths): BM x BN x BK
+//    tiles copied global -> LDS by buffer_load_dwordx4 ... lds (no register
+//    staging) into separate A and B rings, the weight k-tiles further ahead,
+//    XOR-swizzled 16-byte chunks, v_mfma_i32_32x32x32_i8 on a 2x2, 4x2 or
+//    2x4 wave grid; K split over the grid where the tiles alone leave CUs idle.
+//  * gemm_rows (M <= 32, 16-48 weight rows per CU): one block per CU streams
+//    its own weight rows once through 256-byte LDS runs.
+//  * gemm_stream (M <= 16 on the other widths): weight and activation
+//    fragments straight into registers, K split over the block's waves and
+//    the int32 partials added in LDS.
+//  * gemm_tile: register-staged copies into double-buffered, padded LDS;
+//    where K is not a multiple of 64 or an operand reaches 2^31 bytes.
+//  * gemm_skinny: split-K weight streaming with global partials, reachable
+//    only through si_tune_gemm_plan; gemm_i8_scalar: K not a multiple of 32.
 //
 // Fragment layouts: 16x16x64 - lane l holds A row (l%16) / B row (l%16), 16
 // consecutive k starting at 16*(l/16); C lane l holds rows 4*(l/16)+r, r<4, of
