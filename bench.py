@@ -375,30 +375,31 @@ def bench_kv(torch, dev, steps, warmup):
 
     ev_m = (torch.rand(S * H, generator=gen, device=dev) < 0.25)
     ev_u8 = ev_m.to(torch.uint8)
-    ws_b = _native.size_query("si_plan_workspace_bytes", S * H)
-    ws = torch.empty(ws_b, dtype=torch.uint8, device=dev)
+    # PackedKVCache.evict: pass 1 over the old lists (new codes, chunk survivor
+    # counts), the host reads the new sizes from the chunk counts, pass 2
+    # compacts. The timed region holds the two device passes.
+    grp = L0["plan"].device_grouping()
+    o_flat_t = _native.table4([f.data_ptr() for f in grp.flat_lists(S, H)])
+    o_cnt = (ctypes.c_int64 * 4)(*[int(c) for c in grp.counts[:4]])
+    chunks = int(_native.load().si_kv_evict_chunks(o_cnt))
+    cc = torch.empty(max(chunks, 1), dtype=torch.int32, device=dev)
+    bits = torch.empty(max(chunks * int(_native.load().si_kv_evict_chunk_words()), 1),
+                       dtype=torch.int64, device=dev)
     n_code = torch.empty(S * H, dtype=torch.int8, device=dev)
     n_slot = torch.empty(S * H, dtype=torch.int32, device=dev)
-    n_cnt = torch.empty(5, dtype=torch.int64, device=dev)
-    _native.call("si_plan_scan", L0["code"].data_ptr(), ev_u8.data_ptr(), S * H, n_code.data_ptr(),
-                 n_slot.data_ptr(), n_cnt.data_ptr(), ws.data_ptr(), ws_b, sptr)
-    new_counts = [int(c) for c in n_cnt.tolist()]
+    new_counts = grp.evict_count(ev_u8, S, H)[3]
     fresh = cur._alloc_buckets(new_counts, dev, torch.bfloat16)
     ftable = cur._bucket_table(fresh)
-    # PackedKVCache.evict's lists: allocated at the old bucket sizes (which
-    # bound the new ones) before the fused rescan fills them
-    old_counts = [int(c) for c in L0["plan"].device_grouping().counts[:4]]
-    n_flat = [torch.empty(c, dtype=torch.long, device=dev) for c in old_counts]
+    n_flat = [torch.empty(c, dtype=torch.long, device=dev) for c in new_counts[:4]]
     n_flat_t = _native.table4([f.data_ptr() for f in n_flat])
-    n_cap = (ctypes.c_int64 * 4)(*old_counts)
-    n_counts = (ctypes.c_int64 * 5)(*new_counts)
+    n_counts = (ctypes.c_int64 * 4)(*new_counts[:4])
 
-    def evict():  # the device work of PackedKVCache.evict: fused rescan + lists, compaction
-        _native.call("si_plan_scan_lists", L0["code"].data_ptr(), ev_u8.data_ptr(), S, H,
-                     n_code.data_ptr(), n_slot.data_ptr(), n_cnt.data_ptr(), n_flat_t, n_cap,
-                     ws.data_ptr(), ws_b, sptr)
-        _native.call("si_kv_compact_flat", L0["slot"].data_ptr(), L0["table"], n_flat_t, n_counts,
-                     ftable, S, H, B, D, GROUP, L0["sdt"], sptr)
+    def evict():  # the device work of PackedKVCache.evict: count pass, compaction pass
+        _native.call("si_kv_evict_count", L0["code"].data_ptr(), o_flat_t, o_cnt, ev_u8.data_ptr(),
+                     S, H, n_code.data_ptr(), n_slot.data_ptr(), cc.data_ptr(), bits.data_ptr(), sptr)
+        _native.call("si_kv_evict_flat", o_flat_t, o_cnt, cc.data_ptr(), bits.data_ptr(), S, H,
+                     L0["table"], n_flat_t, n_counts, ftable, n_slot.data_ptr(), B, D, GROUP,
+                     L0["sdt"], sptr)
 
     evict()
     ms_ev = timer.time(evict, 20)

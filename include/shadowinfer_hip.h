@@ -224,6 +224,39 @@ int si_kv_compact_flat(const int32_t* old_slot, const void* const* old_buckets,
                        void* const* new_buckets, int64_t S, int64_t H, int64_t B, int64_t D,
                        int64_t group, int scale_dtype, si_stream_t stream);
 
+/* PackedKVCache.evict (packed_kv_cache.py:666-740) over the OLD grouping's
+ * lists, in two passes and without a token-order rescan of the codes. The
+ * old lists old_flat[p] (h*S + t per old slot, old_counts HOST int64[4]) are
+ * cut into chunks of consecutive old slots of one precision;
+ * si_kv_evict_chunks(old_counts) is the number of chunks (-1 on bad sizes)
+ * and si_kv_evict_chunk_words() the uint64 words of survivor bits per chunk.
+ *
+ * si_kv_evict_count: chunk_counts[j] (int32) = survivors of chunk j, and
+ * chunk_bits (chunks * words) their bit masks; new_code[e] = the old code, or
+ * 4 where evict_mask[e] != 0 or the entry was absent (code outside 0..3);
+ * new_slot[e] = -1 for every entry that is not kept. The caller reads
+ * chunk_counts to size the new buckets: the new size of precision p is the
+ * sum over its chunks.
+ *
+ * si_kv_evict_flat: every kept entry gets the new slot (survivors in the
+ * earlier chunks of its precision) + (its rank in its chunk), i.e. the stable
+ * in-bucket compaction; writes new_slot[e], new_flat[p][slot] (lists may be
+ * NULL) and, for precisions whose new bucket pointer is set, the K/V rows
+ * and scales. NULL new bucket pointers leave the precision's rows alone (the
+ * caller keeps the bucket when nothing of it was evicted). new_counts (HOST
+ * int64[4]) bound every slot written. */
+int64_t si_kv_evict_chunks(const int64_t* old_counts);
+int64_t si_kv_evict_chunk_words(void);
+int si_kv_evict_count(const int8_t* old_code, const int64_t* const* old_flat,
+                      const int64_t* old_counts, const uint8_t* evict_mask, int64_t S, int64_t H,
+                      int8_t* new_code, int32_t* new_slot, int32_t* chunk_counts,
+                      uint64_t* chunk_bits, si_stream_t stream);
+int si_kv_evict_flat(const int64_t* const* old_flat, const int64_t* old_counts,
+                     const int32_t* chunk_counts, const uint64_t* chunk_bits, int64_t S, int64_t H,
+                     const void* const* old_buckets, int64_t* const* new_flat,
+                     const int64_t* new_counts, void* const* new_buckets, int32_t* new_slot,
+                     int64_t B, int64_t D, int64_t group, int scale_dtype, si_stream_t stream);
+
 /* Bytes of device workspace si_attn_packed_fwd needs (per-head slot lists). */
 size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv);
 

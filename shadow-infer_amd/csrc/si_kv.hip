@@ -1425,6 +1425,207 @@ int64_t copy_lists_setup(CopyLists& L, const int64_t* const* flat, const int64_t
 }
 
 // ---------------------------------------------------------------------------
+// Evict over the old grouping's lists (si_kv_evict_count + si_kv_evict_flat).
+// Chunk j of the chunk space covers kEvictRows consecutive old slots of one
+// precision (precisions in order 0..3, as the lists). Pass 1 counts the
+// survivors of every chunk and writes the new code of every entry, and slot
+// -1 for the entries that leave or were absent. Pass 2 gives each survivor
+// the new slot
+//   (survivors in the earlier chunks of its precision) + (its rank in the chunk)
+// - the stable in-bucket compaction of packed_kv_cache.py:698-737 - and
+// writes that slot, the new flat list entry and the entry's K/V rows and
+// scales (source rows: consecutive old slots; destination rows: consecutive
+// new slots). No token-order rescan of the codes is needed.
+// ---------------------------------------------------------------------------
+#ifndef SI_EVICT_ROWS
+#define SI_EVICT_ROWS 128
+#endif
+constexpr int kEvictRows = SI_EVICT_ROWS;
+constexpr int kEvictWords = kEvictRows / 64;  // survivor bit words per chunk
+#ifndef SI_EVICT_THREADS
+#define SI_EVICT_THREADS 256
+#endif
+// threads of a pass-2 block: threads past kEvictRows only help with the copy
+constexpr int kEvictThreads = SI_EVICT_THREADS;
+static_assert(kEvictThreads >= kEvictRows && kEvictThreads % 64 == 0, "one thread per row at least");
+constexpr int kEvictFixEntries = 16;          // absent entries: 16 codes per thread
+static_assert(kEvictRows == 128 || kEvictRows == 256, "chunks of 2 or 4 waves");
+
+struct EvictLists {
+  const int64_t* flat[4];  // old grouping: h*S + t per old slot
+  int64_t n[4];            // old bucket sizes
+  int64_t blk_end[4];      // end of each precision's chunks in the chunk space
+};
+
+struct NewLists {
+  int64_t* flat[4];  // new grouping's lists (null: not written)
+  int64_t n[4];      // new bucket sizes
+};
+
+__host__ int64_t evict_lists_setup(EvictLists& L, const int64_t* const* flat, const int64_t* counts) {
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    L.flat[p] = flat[p];
+    L.n[p] = counts[p];
+    acc += ceil_div(counts[p], kEvictRows);
+    L.blk_end[p] = acc;
+  }
+  return acc;
+}
+
+// Precision, first old slot and row count of chunk `blk`.
+__device__ __forceinline__ int evict_chunk(const EvictLists& L, int64_t blk, int64_t* s0, int* rows) {
+  int p = 0;
+  while (p < 3 && blk >= L.blk_end[p]) ++p;
+  *s0 = (blk - (p > 0 ? L.blk_end[p - 1] : 0)) * kEvictRows;
+  *rows = (int)min<int64_t>(kEvictRows, L.n[p] - *s0);
+  return p;
+}
+
+// Blocks [0, chunks): one thread per old slot. Blocks from `chunks` on: the
+// entries that are in no list (code outside 0..3) get code 4 and slot -1.
+__global__ __launch_bounds__(kEvictRows) void kv_evict_count(EvictLists L, int64_t chunks,
+                                                             const int8_t* __restrict__ old_code,
+                                                             const uint8_t* __restrict__ mask,
+                                                             int64_t S, int64_t H,
+                                                             int8_t* __restrict__ new_code,
+                                                             int32_t* __restrict__ new_slot,
+                                                             int32_t* __restrict__ chunk_count,
+                                                             unsigned long long* __restrict__ chunk_bits) {
+  const int64_t blk = blockIdx.x;
+  if (blk >= chunks) {
+    const int64_t n = S * H;
+    const int64_t e0 = ((blk - chunks) * kEvictRows + threadIdx.x) * kEvictFixEntries;
+    if (e0 >= n) return;
+    int8_t c[kEvictFixEntries];
+    if (e0 + kEvictFixEntries <= n && (reinterpret_cast<uintptr_t>(old_code + e0) & 15) == 0) {
+      const uint4 w = *reinterpret_cast<const uint4*>(old_code + e0);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < kEvictFixEntries; ++i) c[i] = (int8_t)(ws[i / 4] >> (8 * (i % 4)));
+    } else {
+#pragma unroll
+      for (int i = 0; i < kEvictFixEntries; ++i) c[i] = e0 + i < n ? old_code[e0 + i] : (int8_t)0;
+    }
+#pragma unroll
+    for (int i = 0; i < kEvictFixEntries; ++i) {
+      if (e0 + i < n && (c[i] < 0 || c[i] > 3)) {
+        new_code[e0 + i] = 4;
+        new_slot[e0 + i] = -1;
+      }
+    }
+    return;
+  }
+  __shared__ unsigned wave_n[kEvictRows / 64];
+  int64_t s0;
+  int rows;
+  const int p = evict_chunk(L, blk, &s0, &rows);
+  bool keep = false;
+  if ((int)threadIdx.x < rows) {
+    const int64_t f = L.flat[p][s0 + threadIdx.x];
+    const uint32_t fu = (uint32_t)f, su = (uint32_t)S;  // S * H < 2^31
+    const int64_t e = (int64_t)(fu % su) * H + (fu / su);
+    keep = mask[e] == 0;
+    new_code[e] = keep ? (int8_t)p : (int8_t)4;
+    if (!keep) new_slot[e] = -1;
+  }
+  const unsigned long long bal = __ballot(keep);
+  if ((threadIdx.x & 63) == 0) {
+    wave_n[threadIdx.x >> 6] = (unsigned)__popcll(bal);
+    chunk_bits[blk * kEvictWords + (threadIdx.x >> 6)] = bal;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned tot = 0;
+#pragma unroll
+    for (int w = 0; w < kEvictWords; ++w) tot += wave_n[w];
+    chunk_count[blk] = (int32_t)tot;
+  }
+}
+
+// One block per chunk, a thread per old slot (and more threads for the copy,
+// as the compaction's blocks have twice the threads of their rows): survivor
+// bits and ranks come
+// from pass 1's ballots, so the chunk counts, the bits and the old list are
+// loaded side by side and the mask is not read again. new_n[p] bounds every
+// slot written; rows are copied only for precisions whose new bucket pointer
+// is set.
+template <bool WIDE>
+__global__ __launch_bounds__(kEvictThreads) void kv_evict_lists(
+    EvictLists L, const int32_t* __restrict__ chunk_count,
+    const unsigned long long* __restrict__ chunk_bits, int64_t S, int64_t H, Buckets dst,
+    Buckets src, RowGeom geo, NewLists nl, int32_t* __restrict__ new_slot) {
+  constexpr int kWaves = kEvictThreads / 64;
+  __shared__ int64_t srcs[kEvictRows];
+  __shared__ int64_t part[kWaves];
+  const int64_t blk = blockIdx.x;
+  int64_t s0;
+  int rows;
+  const int p = evict_chunk(L, blk, &s0, &rows);
+  const int64_t first = p > 0 ? L.blk_end[p - 1] : 0;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  unsigned long long bits[kEvictWords];
+#pragma unroll
+  for (int x = 0; x < kEvictWords; ++x) bits[x] = chunk_bits[blk * kEvictWords + x];
+  const int64_t f = (int)threadIdx.x < rows ? L.flat[p][s0 + threadIdx.x] : -1;
+  // survivors in the earlier chunks of this precision: each thread issues its
+  // loads in batches of 8, so a late chunk of a long list waits for one round
+  // trip per 8 * kEvictRows chunks instead of one per kEvictRows
+  constexpr int kBatch = 8;
+  int64_t acc = 0;
+  for (int64_t j0 = first + threadIdx.x; j0 < blk; j0 += kBatch * kEvictThreads) {
+    int32_t c[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int64_t j = j0 + (int64_t)b * kEvictThreads;
+      c[b] = j < blk ? chunk_count[j] : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) acc += c[b];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) part[w] = acc;
+  unsigned k = 0, tot = 0;
+#pragma unroll
+  for (int x = 0; x < kEvictWords; ++x) {
+    const unsigned c = (unsigned)__popcll(bits[x]);
+    k += x < w ? c : 0u;
+    tot += c;
+  }
+  unsigned long long wb = w == 0 ? bits[0] : 0ull;  // this wave's word (none past the rows)
+#pragma unroll
+  for (int x = 1; x < kEvictWords; ++x) wb = w == x ? bits[x] : wb;
+  const bool keep = ((wb >> lane) & 1ull) != 0 && (int)threadIdx.x < rows;
+  k += (unsigned)__popcll(wb & ((1ull << lane) - 1ull));
+  __syncthreads();
+  int64_t prefix = 0;
+#pragma unroll
+  for (int x = 0; x < kWaves; ++x) prefix += part[x];
+  const int64_t limit = nl.n[p];
+  if (keep) {
+    const int64_t ns = prefix + (int64_t)k;
+    if (ns < limit) {
+      srcs[k] = s0 + threadIdx.x;
+      const uint32_t fu = (uint32_t)f, su = (uint32_t)S;  // S * H < 2^31
+      new_slot[(int64_t)(fu % su) * H + (fu / su)] = (int32_t)ns;
+      if (nl.flat[p] != nullptr) nl.flat[p][ns] = f;
+    }
+  }
+  __syncthreads();
+  const int n_rows = (int)max<int64_t>(0, min<int64_t>((int64_t)tot, limit - prefix));
+  if (n_rows == 0) return;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    copy_rows<WIDE>(dst.p[4 * p + j], src.p[4 * p + j], geo.data_bytes[p], prefix, n_rows, srcs,
+                    nullptr);
+    if (geo.scale_bytes[p] > 0)
+      copy_rows<WIDE>(dst.p[4 * p + 2 + j], src.p[4 * p + 2 + j], geo.scale_bytes[p], prefix,
+                      n_rows, srcs, nullptr);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Token-order reuse (si_kv_reuse, for callers without the plan's flat lists).
 // A block owns kTileEntries consecutive entries e = t*H + h: its threads read
 // their entries' codes, mask and slots with coalesced loads, gather the rows
@@ -2015,6 +2216,107 @@ extern "C" int si_kv_compact_flat(const int32_t* old_slot, const void* const* ol
     kv_copy_lists<false, false><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
         L, dst, to_buckets(old_buckets), nullptr, old_slot, nullptr, S, H, S, geo, nullptr);
   return check_launch("si_kv_compact_flat");
+}
+
+extern "C" int64_t si_kv_evict_chunk_words(void) { return kEvictWords; }
+
+extern "C" int64_t si_kv_evict_chunks(const int64_t* old_counts) {
+  if (old_counts == nullptr) return -1;
+  int64_t acc = 0;
+  for (int p = 0; p < 4; ++p) {
+    if (old_counts[p] < 0) return -1;
+    acc += ceil_div(old_counts[p], (int64_t)kEvictRows);
+  }
+  return acc;
+}
+
+namespace {
+int evict_check_lists(const int64_t* const* old_flat, const int64_t* old_counts, int64_t n,
+                      const char* who) {
+  int64_t listed = 0;
+  for (int p = 0; p < 4; ++p) {
+    SI_CHECK_ARG(old_counts[p] >= 0, "%s: negative bucket size %lld", who, (long long)old_counts[p]);
+    SI_CHECK_ARG(old_counts[p] == 0 || old_flat[p] != nullptr, "%s: NULL list %d", who, p);
+    listed += old_counts[p];
+  }
+  SI_CHECK_ARG(listed <= n, "%s: the lists hold %lld entries, the code matrix %lld", who,
+               (long long)listed, (long long)n);
+  return SI_OK;
+}
+}  // namespace
+
+extern "C" int si_kv_evict_count(const int8_t* old_code, const int64_t* const* old_flat,
+                                 const int64_t* old_counts, const uint8_t* evict_mask, int64_t S,
+                                 int64_t H, int8_t* new_code, int32_t* new_slot,
+                                 int32_t* chunk_counts, uint64_t* chunk_bits, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(S >= 0 && H >= 0, "si_kv_evict_count: negative shape");
+  const int64_t n = S * H;
+  if (n == 0) return SI_OK;
+  SI_CHECK_ARG(old_code && old_flat && old_counts && evict_mask && new_code && new_slot,
+               "si_kv_evict_count: NULL argument");
+  SI_CHECK_ARG(n < ((int64_t)1 << 31), "si_kv_evict_count: %lld entries (slots are int32)",
+               (long long)n);
+  if (int rc = evict_check_lists(old_flat, old_counts, n, "si_kv_evict_count")) return rc;
+  EvictLists L;
+  const int64_t chunks = evict_lists_setup(L, old_flat, old_counts);
+  SI_CHECK_ARG(chunks == 0 || (chunk_counts != nullptr && chunk_bits != nullptr),
+               "si_kv_evict_count: NULL chunk counts or bits");
+  const int64_t fix = ceil_div(n, (int64_t)kEvictRows * kEvictFixEntries);
+  kv_evict_count<<<(unsigned)(chunks + fix), kEvictRows, 0, as_stream(stream)>>>(
+      L, chunks, old_code, evict_mask, S, H, new_code, new_slot, chunk_counts,
+      reinterpret_cast<unsigned long long*>(chunk_bits));
+  return check_launch("si_kv_evict_count");
+}
+
+extern "C" int si_kv_evict_flat(const int64_t* const* old_flat, const int64_t* old_counts,
+                                const int32_t* chunk_counts, const uint64_t* chunk_bits, int64_t S,
+                                int64_t H, const void* const* old_buckets,
+                                int64_t* const* new_flat, const int64_t* new_counts,
+                                void* const* new_buckets, int32_t* new_slot, int64_t B, int64_t D,
+                                int64_t group, int scale_dtype, si_stream_t stream) {
+  clear_error();
+  SI_CHECK_ARG(dtype_ok(scale_dtype), "si_kv_evict_flat: unsupported scale dtype %d", scale_dtype);
+  SI_CHECK_ARG(S >= 0 && H >= 0 && B >= 0 && D > 0, "si_kv_evict_flat: bad shape");
+  SI_CHECK_ARG(group > 0 && D % group == 0, "si_kv_evict_flat: group must divide D");
+  const int64_t n = S * H;
+  if (n == 0) return SI_OK;
+  SI_CHECK_ARG(old_flat && old_counts && old_buckets && new_flat && new_counts && new_buckets &&
+                   new_slot,
+               "si_kv_evict_flat: NULL argument");
+  SI_CHECK_ARG(n < ((int64_t)1 << 31), "si_kv_evict_flat: %lld entries (slots are int32)",
+               (long long)n);
+  if (int rc = evict_check_lists(old_flat, old_counts, n, "si_kv_evict_flat")) return rc;
+  EvictLists L;
+  const int64_t chunks = evict_lists_setup(L, old_flat, old_counts);
+  if (chunks == 0) return SI_OK;
+  SI_CHECK_ARG(chunk_counts != nullptr && chunk_bits != nullptr,
+               "si_kv_evict_flat: NULL chunk counts or bits");
+  NewLists nl;
+  for (int p = 0; p < 4; ++p) {
+    SI_CHECK_ARG(new_counts[p] >= 0 && new_counts[p] <= old_counts[p],
+                 "si_kv_evict_flat: new bucket %d holds %lld rows, the old one %lld", p,
+                 (long long)new_counts[p], (long long)old_counts[p]);
+    nl.flat[p] = new_flat[p];
+    nl.n[p] = new_counts[p];
+    const bool copy = new_buckets[4 * p] != nullptr;
+    for (int j = 0; j < 4; ++j) {
+      if (j >= 2 && p < 2) continue;  // fp32 / fp16 have no scales
+      SI_CHECK_ARG(!copy || (new_buckets[4 * p + j] != nullptr && old_buckets[4 * p + j] != nullptr),
+                   "si_kv_evict_flat: precision %d: NULL bucket tensor %d", p, j);
+    }
+  }
+  const RowGeom geo = make_geom(B, D, group, scale_dtype);
+  const Buckets dst = to_buckets(new_buckets), src = to_buckets(old_buckets);
+  if (B * D * 4 * kEvictRows >= ((int64_t)1 << 32))  // 32-bit unit indices up to here
+    kv_evict_lists<true><<<(unsigned)chunks, kEvictThreads, 0, as_stream(stream)>>>(
+        L, chunk_counts, reinterpret_cast<const unsigned long long*>(chunk_bits), S, H, dst, src,
+        geo, nl, new_slot);
+  else
+    kv_evict_lists<false><<<(unsigned)chunks, kEvictThreads, 0, as_stream(stream)>>>(
+        L, chunk_counts, reinterpret_cast<const unsigned long long*>(chunk_bits), S, H, dst, src,
+        geo, nl, new_slot);
+  return check_launch("si_kv_evict_flat");
 }
 
 namespace {

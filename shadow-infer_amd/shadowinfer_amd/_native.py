@@ -68,6 +68,11 @@ _SIGNATURES = {
     "si_kv_compact": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "si_kv_reuse_flat": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                                 _i64, _i32, _vp, _vp]),
+    "si_kv_evict_chunks": (_i64, [_vp]),
+    "si_kv_evict_chunk_words": (_i64, []),
+    "si_kv_evict_count": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "si_kv_evict_flat": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64,
+                                _i64, _i64, _i32, _vp]),
     "si_kv_compact_flat": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                   _vp]),
     "si_attn_workspace_bytes": (_sz, [_i64, _i64]),

@@ -349,32 +349,33 @@ class PackedKVCache:
                 return 0
         old = self._grouping
         dev = old.code.device
-        new = old.rescan(mask.to(dev), self.seq_len, self.num_heads)
-        removed = int(sum(old.counts[:4]) - sum(new.counts[:4]))
+        S, H = self.seq_len, self.num_heads
+        mask = mask.to(dev)
+        code, slot, (chunk_counts, chunk_bits), counts = old.evict_count(mask, S, H)
+        removed = int(sum(old.counts[:4]) - sum(counts[:4]))
         if removed == 0:
             return 0
         new_buckets: Dict[str, Dict[str, Any]] = {}
         changed: Dict[str, Dict[str, Any]] = {}
-        fresh = self._alloc_buckets(new.counts, dev, self._scale_dtype)
+        fresh = self._alloc_buckets(counts, dev, self._scale_dtype)
         for name in PRECISION_ORDER:
             p = _PREC_INDEX[name]
-            if new.counts[p] == 0:
+            if counts[p] == 0:
                 continue
-            if new.counts[p] == old.counts[p]:
+            if counts[p] == old.counts[p]:
                 new_buckets[name] = self._buckets[name]  # untouched (reference keeps it)
             else:
                 new_buckets[name] = fresh[name]
                 changed[name] = fresh[name]
-        if changed:
-            flat = new.flat_lists(self.seq_len, self.num_heads)
-            _native.call("si_kv_compact_flat", old.slot.data_ptr(), self._bucket_table(),
-                         _native.table4([f.data_ptr() for f in flat]),
-                         (ctypes.c_int64 * 5)(*new.counts), self._bucket_table(changed),
-                         self.seq_len, self.num_heads, self.batch_size, self.head_dim,
-                         self._group_size, _native.dtype_code(self._scale_dtype),
-                         _native.stream(dev))
+        flat = [torch.empty(c, dtype=torch.long, device=dev) for c in counts[:4]]
+        _native.call("si_kv_evict_flat", _native.table4([f.data_ptr() for f in old.flat_lists(S, H)]),
+                     (ctypes.c_int64 * 4)(*old.counts[:4]), chunk_counts.data_ptr(),
+                     chunk_bits.data_ptr(), S, H, self._bucket_table(), _native.table4([f.data_ptr() for f in flat]),
+                     (ctypes.c_int64 * 4)(*counts[:4]), self._bucket_table(changed), slot.data_ptr(),
+                     self.batch_size, self.head_dim, self._group_size,
+                     _native.dtype_code(self._scale_dtype), _native.stream(dev))
         self._buckets = new_buckets
-        self._grouping = new
+        self._grouping = DeviceGrouping(code, slot, counts, flat)
         self._view = None
         return removed
 

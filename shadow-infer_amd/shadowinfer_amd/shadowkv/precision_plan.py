@@ -176,26 +176,34 @@ class DeviceGrouping:
                      counts.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream(dev))
         return DeviceGrouping(code, slot, [int(c) for c in counts.tolist()])
 
-    def rescan(self, evict_mask: torch.Tensor, S: int, H: int) -> "DeviceGrouping":
-        """The grouping without the entries ``evict_mask`` marks, flat lists
-        included, in one fused pass (si_plan_scan_lists). The lists are
-        allocated at this grouping's bucket sizes, which bound the new ones,
-        and returned as views of the new sizes."""
+    def evict_count(self, evict_mask: torch.Tensor, S: int, H: int):
+        """First pass of an evict (si_kv_evict_count) over this grouping's
+        lists: returns the new codes, the new slot array (-1 already written
+        for every entry that is not kept), the per-chunk survivor counts and
+        bits on the device, and the new bucket sizes (host ints, code 4 last),
+        read from those counts."""
         dev = self.code.device
         n = S * H
-        ws_bytes = _native.size_query("si_plan_workspace_bytes", n)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        flat = self.flat_lists(S, H)
+        lib = _native.load()
+        old = (ctypes.c_int64 * 4)(*self.counts[:4])
+        chunks = int(lib.si_kv_evict_chunks(old))
+        words = int(lib.si_kv_evict_chunk_words())
         code = torch.empty(n, dtype=torch.int8, device=dev)
         slot = torch.empty(n, dtype=torch.int32, device=dev)
-        counts = torch.empty(5, dtype=torch.int64, device=dev)
-        cap = [int(c) for c in self.counts[:4]]
-        full = [torch.empty(c, dtype=torch.long, device=dev) for c in cap]
-        _native.call("si_plan_scan_lists", self.code.data_ptr(), evict_mask.data_ptr(), S, H,
-                     code.data_ptr(), slot.data_ptr(), counts.data_ptr(),
-                     _native.table4([f.data_ptr() for f in full]), (ctypes.c_int64 * 4)(*cap),
-                     ws.data_ptr(), ws_bytes, _native.stream(dev))
-        new_counts = [int(c) for c in counts.tolist()]
-        return DeviceGrouping(code, slot, new_counts, [f[:c] for f, c in zip(full, new_counts)])
+        cc = torch.empty(max(chunks, 1), dtype=torch.int32, device=dev)
+        bits = torch.empty(max(chunks * words, 1), dtype=torch.int64, device=dev)
+        _native.call("si_kv_evict_count", self.code.data_ptr(),
+                     _native.table4([f.data_ptr() for f in flat]), old, evict_mask.data_ptr(), S, H,
+                     code.data_ptr(), slot.data_ptr(), cc.data_ptr(), bits.data_ptr(),
+                     _native.stream(dev))
+        per = cc[:chunks].cpu().numpy().astype(np.int64)
+        rows = 64 * words
+        ends = np.cumsum([-(-c // rows) for c in self.counts[:4]])
+        starts = np.concatenate(([0], ends[:-1]))
+        new_counts = [int(per[a:b].sum()) for a, b in zip(starts, ends)]
+        new_counts.append(n - sum(new_counts))
+        return code, slot, (cc, bits), new_counts
 
 
 class PrecisionPlan:

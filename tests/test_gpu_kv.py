@@ -82,6 +82,89 @@ def test_plan_scan_lists_matches_scan_then_scatter(dev, S, H):
         assert bool((bufs[p][cap[p]:] == -7).all())
 
 
+@pytest.mark.parametrize("S,H,B,D,dtype,whole", [(7, 3, 1, 32, torch.float32, False),
+                                                  (300, 8, 2, 64, torch.bfloat16, True),
+                                                  (1000, 5, 1, 45, torch.float16, False),
+                                                  (2048, 32, 1, 128, torch.bfloat16, False)])
+def test_evict_passes_match_rescan_and_compaction(dev, S, H, B, D, dtype, whole):
+    """si_kv_evict_count + si_kv_evict_flat (the passes PackedKVCache.evict
+    runs) give the codes, slots and sizes of si_plan_scan with the mask, the
+    lists of si_plan_scatter and the buckets of si_kv_compact_flat. Unknown
+    codes (-1, 5) and absent entries come out as code 4 / slot -1; no list is
+    written past its new size; a precision with nothing evicted (NULL new
+    bucket pointer) keeps its rows; ``whole`` evicts every int4 entry."""
+    import ctypes
+    from shadowinfer_amd import _native
+    from shadowinfer_amd.shadowkv.precision_plan import DeviceGrouping
+    k, v = kv_inputs(B, H, S, D, dtype, seed=S)
+    codes = mixed_codes(S, H, seed=S + 5, probs=(1, 1, 1, 1), evicted=0.1)
+    plan = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))
+    cache = PackedKVCache.pack(k.to(dev), v.to(dev), None, plan=plan)["packed_kv"]
+    code, slot, table, sdt, g = cache.device_state()
+    grp = cache._grouping
+    n = S * H
+    rng = np.random.default_rng(S * 7 + H)
+    cnp = code.cpu().numpy()
+    m = rng.random(n) < 0.3
+    m[cnp == 0] = False          # fp32: nothing evicted, bucket kept as it is
+    if whole:
+        m[cnp == 3] = True
+    mask = torch.from_numpy(m.astype(np.uint8)).to(dev)
+    raw = code.clone()             # absent entries given unknown codes too
+    absent = np.nonzero(cnp == 4)[0]
+    raw[torch.from_numpy(absent[::2]).to(dev)] = -1
+    raw[torch.from_numpy(absent[1::2]).to(dev)] = 5
+    ref = DeviceGrouping.scan(code, evict_mask=mask)
+    ref_flat = ref.flat_lists(S, H)
+    sp = _native.stream(dev)
+    lib = _native.load()
+    old_cnt = (ctypes.c_int64 * 4)(*grp.counts[:4])
+    chunks = int(lib.si_kv_evict_chunks(old_cnt))
+    words = int(lib.si_kv_evict_chunk_words())
+    rows = 64 * words
+    assert chunks == sum(-(-c // rows) for c in grp.counts[:4])
+    cc = torch.full((max(chunks, 1),), -5, dtype=torch.int32, device=dev)
+    bits = torch.full((max(chunks * words, 1),), -5, dtype=torch.int64, device=dev)
+    ncode = torch.full((n,), 9, dtype=torch.int8, device=dev)
+    nslot = torch.full((n,), -9, dtype=torch.int32, device=dev)
+    old_flat = _native.table4([f.data_ptr() for f in grp.flat_lists(S, H)])
+    _native.call("si_kv_evict_count", raw.data_ptr(), old_flat, old_cnt, mask.data_ptr(), S, H,
+                 ncode.data_ptr(), nslot.data_ptr(), cc.data_ptr(), bits.data_ptr(), sp)
+    per = cc[:chunks].cpu().numpy().astype(np.int64)
+    pop = [bin(int(x) & (2**64 - 1)).count("1") for x in bits[: chunks * words].cpu().tolist()]
+    assert per.tolist() == [sum(pop[words * j: words * j + words]) for j in range(chunks)]
+    ends = np.cumsum([-(-c // rows) for c in grp.counts[:4]])
+    counts = [int(per[a:b].sum()) for a, b in zip(np.concatenate(([0], ends[:-1])), ends)]
+    assert counts == ref.counts[:4]
+    assert counts[0] == grp.counts[0] and (not whole or counts[3] == 0)
+
+    def changed_buckets():
+        fresh = cache._alloc_buckets(ref.counts, dev, cache._scale_dtype)
+        return {name: fresh[name] for name in fresh
+                if 0 < ref.counts[_IDX[name]] < grp.counts[_IDX[name]]}
+
+    mine, theirs = changed_buckets(), changed_buckets()
+    nflat = [torch.full((c + 4,), -7, dtype=torch.long, device=dev) for c in counts]
+    _native.call("si_kv_evict_flat", old_flat, old_cnt, cc.data_ptr(), bits.data_ptr(), S, H, table,
+                 _native.table4([f.data_ptr() for f in nflat]), (ctypes.c_int64 * 4)(*counts),
+                 cache._bucket_table(mine), nslot.data_ptr(), B, D, g, sdt, sp)
+    _native.call("si_kv_compact_flat", slot.data_ptr(), table,
+                 _native.table4([f.data_ptr() for f in ref_flat]), (ctypes.c_int64 * 5)(*ref.counts),
+                 cache._bucket_table(theirs), S, H, B, D, g, sdt, sp)
+    assert torch.equal(ncode, ref.code) and torch.equal(nslot, ref.slot)
+    for p in range(4):
+        assert torch.equal(nflat[p][: counts[p]], ref_flat[p]), p
+        assert bool((nflat[p][counts[p]:] == -7).all()), p
+    assert set(mine) == set(theirs) and "fp32" not in mine
+    for name, d in mine.items():
+        for key, t in d.items():
+            if torch.is_tensor(t):
+                assert torch.equal(t.view(torch.uint8), theirs[name][key].view(torch.uint8)), (name, key)
+
+
+_IDX = {"fp32": 0, "fp16": 1, "int8": 2, "int4": 3}
+
+
 def test_plan_device_matches_host_plan(dev):
     codes = mixed_codes(300, 5, seed=3, probs=(1, 1, 1, 1), evicted=0.1)
     gpu = PrecisionPlan.from_codes(torch.from_numpy(codes).to(dev))

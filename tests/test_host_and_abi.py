@@ -300,7 +300,17 @@ def test_step_and_copy_entry_points_reject_bad_arguments():
     t4 = _native.table4([None] * 4)
     t16 = _native.table16([None] * 16)
     c5 = (ctypes.c_int64 * 5)(0, 1, 0, 0, 0)
+    c4 = (ctypes.c_int64 * 4)(0, 1, 3, 0)
+    big = (ctypes.c_int64 * 4)(0, 9, 9, 0)   # 18 listed entries in an 8 x 2 matrix
+    grow = (ctypes.c_int64 * 4)(0, 2, 3, 0)  # more rows than the old bucket
+    l4 = _native.table4([None, 16, 16, None])
+    k_only = _native.table16([None] * 8 + [16, 16, None, None] + [None] * 4)  # int8 without scales
     f = ctypes.c_float
+    rows = 64 * lib.si_kv_evict_chunk_words()
+    assert rows in (128, 256)
+    assert lib.si_kv_evict_chunks(c4) == 2 and lib.si_kv_evict_chunks(null) == -1
+    assert lib.si_kv_evict_chunks((ctypes.c_int64 * 4)(0, -1, 0, 0)) == -1
+    assert lib.si_kv_evict_chunks((ctypes.c_int64 * 4)(rows, rows + 1, 0, 1)) == 4
     checks = [
         # K not a multiple of 8 / above the register budget / q without scale
         (lambda: lib.si_rmsnorm_rows(16, 2, 4, 12, 16, f(1e-5), 16, null, null, null), b"multiple of 8"),
@@ -317,6 +327,17 @@ def test_step_and_copy_entry_points_reject_bad_arguments():
         (lambda: lib.si_kv_reuse_flat(t4, c5, t16, 8, 1, 1, t16, 8, 1, 2, 1, 64, 48, 2, null, null), b"group"),
         (lambda: lib.si_kv_reuse_flat(t4, c5, t16, 8, 1, 1, t16, 8, null, 2, 1, 64, 16, 2, null, null), b"NULL"),
         (lambda: lib.si_kv_compact_flat(1, t16, t4, c5, t16, 8, 2, 1, 64, 16, 9, null), b"scale dtype"),
+        # evict passes: missing arguments, inconsistent sizes, absent scale tensors
+        (lambda: lib.si_kv_evict_count(16, t4, c4, null, 8, 2, 16, 16, 16, 16, null), b"NULL"),
+        (lambda: lib.si_kv_evict_count(16, t4, c4, 16, 8, 2, 16, 16, 16, 16, null), b"NULL list"),
+        (lambda: lib.si_kv_evict_count(16, l4, big, 16, 8, 2, 16, 16, 16, 16, null), b"lists hold"),
+        (lambda: lib.si_kv_evict_count(16, l4, c4, 16, 8, 2, 16, 16, 16, null, null), b"bits"),
+        (lambda: lib.si_kv_evict_flat(l4, c4, 16, 16, 8, 2, t16, t4, grow, t16, 16, 1, 64, 16, 2, null),
+         b"new bucket 1"),
+        (lambda: lib.si_kv_evict_flat(l4, c4, 16, 16, 8, 2, t16, t4, c4, k_only, 16, 1, 64, 16, 2, null),
+         b"NULL bucket tensor"),
+        (lambda: lib.si_kv_evict_flat(l4, c4, 16, 16, 8, 2, t16, t4, c4, t16, 16, 1, 64, 48, 2, null),
+         b"group"),
         (lambda: lib.si_page_write_pages(16, 16, 2, 1, 2, 8, 64, 0, 2, 2, 16, t4, 8, null), b"outside"),
         (lambda: lib.si_page_write_pages(16, 16, 2, 1, 2, 64, 64, 0, 2, 5, 16, t4, 8, null), b"precision"),
         (lambda: lib.si_attn_build_lists(1, 1, 2, 64, 16, 7, null), b"workspace"),
@@ -332,6 +353,9 @@ def test_step_and_copy_entry_points_reject_bad_arguments():
     assert lib.si_swiglu_quant(null, 2, 0, 64, null, null, null, null) == 0
     assert lib.si_rope_split(null, 2, 0, 8, 4, 64, null, null, null, null, null, null) == 0
     assert lib.si_kv_compact_flat(1, t16, t4, c5, t16, 0, 2, 1, 64, 16, 2, null) == 0
+    assert lib.si_kv_evict_count(null, null, null, null, 0, 2, null, null, null, null, null) == 0
+    assert lib.si_kv_evict_flat(null, null, null, null, 8, 0, null, null, null, null, null, 1, 64, 16,
+                                2, null) == 0
 
 
 def test_token_head_masks_follow_python_membership():
