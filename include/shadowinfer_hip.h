@@ -266,7 +266,8 @@ size_t si_attn_workspace_bytes(int64_t H, int64_t S_kv);
  * Semantic neighbour of shadowinfer/kernels/__init__.py:473-537.
  * q: [B, H, S_q, D], q_dtype SI_DT_BF16 or SI_DT_F16, 16-byte aligned; D = 64
  * or 128; group: int4 group size (a multiple of D/16 dividing D).
- * out: [B, H, S_q, D] in out_dtype (SI_DT_F32 matches unpack()'s fp32 K/V).
+ * out: [B, H, S_q, D] in out_dtype (SI_DT_F32 matches unpack()'s fp32 K/V),
+ * 16-byte aligned.
  * workspace: si_attn_workspace_bytes(H, S_kv) bytes, 16-byte aligned. */
 int si_attn_packed_fwd(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q,
                        int64_t D, const int8_t* code, const int32_t* slot,

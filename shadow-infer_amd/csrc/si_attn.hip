@@ -146,6 +146,13 @@ struct AttnCfg {
   // the 8-byte reads of the four rows and two 16-dim halves one transposed
   // read of 32 lanes covers on 64 distinct banks.
   static constexpr int VROW = D == 128 ? 160 : 96;
+  // Output staging (finish_rows): a wave's 32 rows pass through LDS in chunks
+  // of SRB bytes per row (pitch SRB + 16), so every global store instruction
+  // writes whole contiguous row pieces. Waves 0-3 stage in the K tile
+  // buffers, waves 4-7 in the V tile buffers (both free after the last tile).
+  static constexpr int SRB = D == 128 ? 256 : 128;
+  static constexpr int SPITCH = SRB + 16;
+  static constexpr int STAGE = 32 * SPITCH;  // bytes per wave
 };
 
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -409,12 +416,23 @@ __device__ __forceinline__ void load_q(const uint16_t* __restrict__ Q, int64_t b
 }
 
 // Evicted / absent keys (score 0, value 0) join the softmax denominator
-// (n_ev * 2^(0 - m)); then row m of O^T, divided by the row sum, is stored
-// at out + obase in out_dtype.
+// (n_ev * 2^(0 - m)); then the wave's rows of O^T, divided by their row sums
+// and rounded to out_dtype, go to out. Lane l holds dims db*32 + 8i + 4*grp
+// .. +3 of query l % 32, so direct stores would scatter 8- or 16-byte pieces
+// over 32 rows; instead the rows are staged in LDS (chunks of SRB bytes per
+// row) and read back row-contiguous: each store instruction writes 64 x 16
+// contiguous bytes of SRB / 16 lanes per row. Row r of the wave is query
+// m0 + r at out + obase0 + r * row_stride (elements); rows at or past Sq are
+// not stored.
 template <int D>
-__device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, int n_ev,
-                                            bool m_ok, int64_t obase, int grp, void* O, int odt) {
+__device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, int n_ev, int col,
+                                            int grp, uint8_t* stage, int64_t m0, int64_t Sq,
+                                            int64_t obase0, int64_t row_stride, void* O,
+                                            int odt) {
+  using C = AttnCfg<D>;
   constexpr int DB = D / 32;
+  constexpr int CPR = C::SRB / 16;  // 16-byte chunks per staged row
+  const int lane = (grp << 5) | col;
   l_run = halves_sum(l_run);  // each half summed its own keys
   if (n_ev > 0) {
     const float m_fin = fmaxf(m_run, 0.0f);
@@ -425,27 +443,55 @@ __device__ __forceinline__ void finish_rows(v16f* o, float m_run, float l_run, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
   }
-  if (!m_ok) return;
-  const float inv = 1.0f / l_run;
+  const float inv = 1.0f / l_run;  // rows past Sq may divide by 0: never stored
+  auto store_chunks = [&](int es, int pd0) __attribute__((always_inline)) {
+    __builtin_amdgcn_wave_barrier();
+    uint8_t* ob = reinterpret_cast<uint8_t*>(O);
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+    for (int j = 0; j < CPR / 2; ++j) {
+      const int idx = j * 64 + lane;
+      const int r = idx / CPR, c = idx % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * C::SPITCH + c * 16);
+      if (m0 + r < Sq)
+        *reinterpret_cast<uint4*>(ob + (obase0 + (int64_t)r * row_stride + pd0) * es + c * 16) = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+  if (odt == SI_DT_F32) {
+    constexpr int DPP = C::SRB / 4;  // dims per pass
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = db * 32 + 8 * i + 4 * grp;
-      const float r0 = o[db][4 * i + 0] * inv, r1 = o[db][4 * i + 1] * inv;
-      const float r2 = o[db][4 * i + 2] * inv, r3 = o[db][4 * i + 3] * inv;
-      if (odt == SI_DT_F32) {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(O) + obase + d) =
-            make_float4(r0, r1, r2, r3);
-      } else {
-        const bool bf = odt == SI_DT_BF16;
+    for (int pd0 = 0; pd0 < D; pd0 += DPP) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = db * 32 + 8 * i + 4 * grp;
+          if (db * 32 >= pd0 && db * 32 < pd0 + DPP)
+            *reinterpret_cast<float4*>(stage + col * C::SPITCH + (d - pd0) * 4) =
+                make_float4(o[db][4 * i] * inv, o[db][4 * i + 1] * inv, o[db][4 * i + 2] * inv,
+                            o[db][4 * i + 3] * inv);
+        }
+      }
+      store_chunks(4, pd0);
+    }
+  } else {
+    static_assert(C::SRB == 2 * D, "one pass of 16-bit rows");
+    const bool bf = odt == SI_DT_BF16;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = db * 32 + 8 * i + 4 * grp;
+        const float r0 = o[db][4 * i + 0] * inv, r1 = o[db][4 * i + 1] * inv;
+        const float r2 = o[db][4 * i + 2] * inv, r3 = o[db][4 * i + 3] * inv;
         const uint32_t w0 = (bf ? f32_to_bf16_bits(r0) : f32_to_f16_bits(r0)) |
                             ((bf ? f32_to_bf16_bits(r1) : f32_to_f16_bits(r1)) << 16);
         const uint32_t w1 = (bf ? f32_to_bf16_bits(r2) : f32_to_f16_bits(r2)) |
                             ((bf ? f32_to_bf16_bits(r3) : f32_to_f16_bits(r3)) << 16);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(O) + obase + d) = make_uint2(w0, w1);
+        *reinterpret_cast<uint2*>(stage + col * C::SPITCH + d * 2) = make_uint2(w0, w1);
       }
     }
+    store_chunks(2, 0);
   }
 }
 
@@ -506,10 +552,14 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   const int wave = tid >> 6;
   const int col = lane & 31;  // query column within the wave
   const int grp = lane >> 5;  // 0/1: k-half of MFMA operands, row quad of results
-  const int64_t h = blockIdx.y;
-  const int64_t b = blockIdx.z;
-  const int64_t m = (int64_t)blockIdx.x * C::BMQ + wave * 32 + col;
-  const bool m_ok = m < Sq;
+  // The query blocks of one (b, h) on one XCD, one after another in dispatch
+  // order, so the head's packed K/V is fetched into that XCD's L2 once.
+  const int nq = (int)gridDim.x;
+  const int w_id = xcd_order((int)(blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z)),
+                             nq * (int)(gridDim.y * gridDim.z));
+  const int64_t h = (w_id / nq) % (int)gridDim.y;
+  const int64_t b = w_id / (nq * (int)gridDim.y);
+  const int64_t m = (int64_t)(w_id % nq) * C::BMQ + wave * 32 + col;
 
   // Q^T fragments (B operand of S^T = K Q^T): query m, dims ks*16 + 8*grp + 0..7.
   v8h qf[KS];
@@ -803,7 +853,14 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   run_phase(std::integral_constant<int, SI_PREC_INT8>{});
   run_phase(std::integral_constant<int, SI_PREC_INT4>{});
 
-  finish_rows<D>(o, m_run, l_run, n_ev, m_ok, b * os.b + h * os.h + m * os.s, grp, O, odt);
+  // Every wave is past the last tile's barrier: the tile buffers are free.
+  static_assert(4 * C::STAGE <= (int)sizeof(Ks) && 4 * C::STAGE <= (int)sizeof(Vs),
+                "output staging fits the tile buffers");
+  uint8_t* stage = wave < 4 ? reinterpret_cast<uint8_t*>(&Ks[0][0][0]) + wave * C::STAGE
+                            : reinterpret_cast<uint8_t*>(&Vs[0][0][0]) + (wave - 4) * C::STAGE;
+  const int64_t m0 = m - col;
+  finish_rows<D>(o, m_run, l_run, n_ev, col, grp, stage, m0, Sq, b * os.b + h * os.h + m0 * os.s,
+                 os.s, O, odt);
 }
 
 template <int D, int QDT, bool O32>
@@ -889,8 +946,9 @@ int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int6
                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
                "si_attn_packed_fwd: workspace too small or misaligned (%zu < %zu bytes)",
                workspace_bytes, need);
-  SI_CHECK_ARG((reinterpret_cast<uintptr_t>(q) & 15) == 0,
-               "si_attn_packed_fwd: q must be 16-byte aligned");
+  SI_CHECK_ARG((reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "si_attn_packed_fwd: q and out must be 16-byte aligned");
   const Buckets bk = to_buckets(buckets);
   const int64_t cap = list_cap(S_kv);
   int32_t* counts = reinterpret_cast<int32_t*>(workspace);
@@ -900,6 +958,9 @@ int run_attn(const void* q, int q_dtype, int64_t B, int64_t H, int64_t S_q, int6
     if (int rc = check_launch("si_attn_packed_fwd")) return rc;
   }
   const int64_t bmq = D == 128 ? AttnCfg<128>::BMQ : AttnCfg<64>::BMQ;
+  SI_CHECK_ARG(ceil_div(S_q, bmq) * H * B < ((int64_t)1 << 31),
+               "si_attn_packed_fwd: %lld query blocks (at most 2^31 - 1)",
+               (long long)(ceil_div(S_q, bmq) * H * B));
   const dim3 grid((unsigned)ceil_div(S_q, bmq), (unsigned)H, (unsigned)B);
   const float scale_log2 = sm_scale * 1.4426950408889634f;
   const uint16_t* qp = reinterpret_cast<const uint16_t*>(q);

@@ -40,6 +40,18 @@ inline int dtype_size(int dt) { return dt == SI_DT_F32 ? 4 : 2; }
 
 // ---- scalar conversions (device) -------------------------------------------
 
+// Workgroups are dispatched round-robin over the 8 XCDs (linear id b goes to
+// XCD b % 8). xcd_order renumbers a grid of n workgroups so that each XCD
+// receives a contiguous run of ids, in dispatch order; consecutive ids that
+// read the same data then share one L2.
+__device__ __forceinline__ int xcd_order(int b, int n) {
+  constexpr int X = 8;
+  const int per = (n + X - 1) / X;     // ids on each of the first `tall` XCDs
+  const int tall = n - (per - 1) * X;  // 1..8
+  const int x = b % X, j = b / X;
+  return x < tall ? x * per + j : tall * per + (x - tall) * (per - 1) + j;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }

@@ -359,16 +359,8 @@ __device__ __forceinline__ void wait_tiles(int n) {
   }
 }
 
-// Workgroups are dispatched round-robin over the 8 XCDs. Renumber them so
-// that each XCD receives a contiguous run of tile ids: with M-tiles fastest,
-// the tiles that read the same weight columns then share one L2.
-__device__ __forceinline__ int xcd_order(int b, int n) {
-  constexpr int X = 8;
-  const int per = (n + X - 1) / X;     // tiles on each of the first `tall` XCDs
-  const int tall = n - (per - 1) * X;  // 1..8
-  const int x = b % X, j = b / X;
-  return x < tall ? x * per + j : tall * per + (x - tall) * (per - 1) + j;
-}
+// xcd_order (si_common.h): with M-tiles fastest, the tiles that read the same
+// weight columns share one XCD's L2.
 
 // 8 consecutive values of type ODT at element idx (16- or 32-byte aligned).
 template <int ODT>

@@ -104,6 +104,9 @@ def test_argument_validation_needs_no_device():
     rc = lib.si_attn_packed_fwd(16, 2, 1, 2, 8, 64, 1, 1, table, 2, 64, 16, ctypes.c_float(0.1), 16, 0,
                                 16, ws - 1, null)
     assert rc == 1 and b"workspace" in lib.si_last_error()
+    rc = lib.si_attn_packed_fwd(16, 2, 1, 2, 8, 64, 1, 1, table, 2, 64, 16, ctypes.c_float(0.1), 24, 0,
+                                16, ws, null)  # out 8-byte aligned: the staged rows store 16 bytes
+    assert rc == 1 and b"16-byte aligned" in lib.si_last_error()
     assert lib.si_int4_unpack_rows(1, 1, 2, 5, 1, null) == 1  # 2 bytes hold at most 4 codes
     with pytest.raises(ValueError, match="si_kv_unpack"):
         _native.call("si_kv_unpack", 1, 1, table, 2, 1, 1, 1, 64, 48, 1, 1, None)
