@@ -535,7 +535,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
                                                          int32_t* __restrict__ Cout, EpiArgs ep) {
   constexpr int NW = WM * WN;  // 4 waves (one per SIMD) or 8 (two per SIMD)
   static_assert(NW == 4 || NW == 8, "four or eight waves per block");
-  static_assert(RA >= 2 && (RA == RB || (RA == 2 && RB > 2)), "equal rings, or A in 2 slots");
+  static_assert(RA >= 2 && RB >= RA, "A ring no deeper than the B ring");
   constexpr int CPR = BK / 16;
   constexpr int LA = BM * BK / 1024 / NW;  // 1-KB DMA blocks of A per wave per k-tile
   constexpr int LB = BN * BK / 1024 / NW;
@@ -550,7 +550,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
   static_assert(KS % 2 == 0, "fragment buffers alternate per k-slice");
   constexpr int EP = TN + 8;  // epilogue staging pitch in words (rows r and r+4 on other banks)
   static_assert(NW * 16 * EP * 4 <= LDS_BYTES, "epilogue staging fits in the rings");
-  static_assert(RA == RB ? (RA - 2) * LPT <= 63 : (RB - 2) * LB <= 63, "vmcnt range");
+  static_assert(RA == RB ? (RA - 2) * LPT <= 63
+                         : (RB - 2) * LB <= 63 && LB + (RA - 2) * (LA + LB) <= 63,
+                "vmcnt range");
   __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
   int8_t* const ldsA = lds;
   int8_t* const ldsB = lds + RA * ASZ;
@@ -604,17 +606,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma(const int8_t* __restric
   };
   // This wave's copies of A(t+1) and B(t+1) have landed and its LDS reads are
   // complete (called at the end of iteration t; t = -1 before the loop).
+  // Copies complete in issue order, so waiting until at most N are in flight
+  // is safe whenever at least N were issued after A(t+1); B(t+1) is issued
+  // before A(t+1) when RB > RA.
   auto wait_next = [&](int t) {
     if constexpr (RA == RB) {
       // iteration u issued A(u+RA-1), B(u+RA-1): up to RA-2 later k-tiles may fly
       wait_tiles<LPT, RA>(min(nk - 2 - t, RA - 2));
     } else if (t < 0) {
-      // prologue issued A(0), B(0), then B(1) .. B(RB-2)
+      // prologue issued A(j), B(j) for j < RA-1, then B(RA-1) .. B(RB-2), in
+      // k order: B(1) .. B(min(RB-2, nk-1)) came after A(0) and B(0)
       wait_tiles<LB, RB>(min(nk - 1, RB - 2));
+    } else if (t + RB - 1 < nk) {
+      // A(t+1) was followed by the B k-tile of its iteration and by an A and a
+      // B k-tile in each of the RA-2 later iterations
+      wait_cnt<LB + (RA - 2) * (LA + LB), 0>();
     } else {
-      // iteration t issued A(t+1), then B(t+RB-1) (if any), which may fly
-      if (t + RB - 1 < nk) wait_cnt<LB, 0>();
-      else wait_cnt<0, 0>();
+      // near the end: count only the A k-tiles issued after A(t+1)
+      wait_tiles<LA, RA>(max(0, min(t + RA - 1, nk - 1) - t - 1));
     }
   };
 
