@@ -565,6 +565,14 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   v8h qf[KS];
   load_q<D, QDT>(Q, b, H, h, Sq, m, grp, scale_log2, qf);
 
+  // Slots of tile 0, loaded beside the head's counts: the first non-empty
+  // precision phase always starts at tile 0, so its first slot load does not
+  // wait for the counts (the list holds at least 4 tiles, so the read is in
+  // bounds even when every key of the head is evicted).
+  const int32_t* lh = lists + h * cap;
+  const int kg = tid / C::DGN;
+  const int4 sl0 = *reinterpret_cast<const int4*>(lh + 4 * kg);
+
   // Tile schedule: the head's list regions in order fp32, fp16, int8, int4.
   const int32_t* cnt = counts + h * 8;
   int np[4], tstart[5];
@@ -575,17 +583,15 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     tstart[p + 1] = tstart[p] + (np[p] + BN - 1) / BN;
   }
   const int n_ev = cnt[4];
-  const int32_t* lh = lists + h * cap;
   auto tile_valid = [&](int tt, int p) __attribute__((always_inline)) { return min(BN, np[p] - (tt - tstart[p]) * BN); };
 
   // Decode-stage coordinates: keys 4*kg .. 4*kg+3 of the tile, dims d0 .. d0+DPT-1.
-  const int kg = tid / C::DGN;
   const int dg = tid % C::DGN;
   const int d0 = dg * DPT;
   const int ngrp = (int)(D / g);       // int4 groups per row
   const int my_grp = d0 / (int)g;      // this thread's group (DPT values never straddle one)
 
-  int4 sl = make_int4(0, 0, 0, 0);  // slots of the next tile to fetch
+  int4 sl = sl0;                    // slots of the next tile to fetch
   int4 sl_data = sl;                 // slots of the tile held in rk / rv
   uint32_t rk[4][RW], rv[4][RW];
   uint32_t skb[4], svb[4];  // raw scale bits, converted at decode time
@@ -828,7 +834,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     const int t0 = tstart[P], t1 = tstart[P + 1];
     if (t0 >= t1) return;
     t_last = t1 - 1;
-    fetch_slots(t0);
+    if (t0 > 0) fetch_slots(t0);  // tile 0's slots were loaded at the start
     fetch_data(PC, t0);
     fetch_slots(t0 + 1);
     decode_tile(PC, t0, buf);
