@@ -829,13 +829,19 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   };
 
   int buf = 0;
+  // Slots of the first tile of the next non-empty phase: loaded when a phase
+  // starts (clamped to the head's last tile, so always in bounds), they have
+  // landed by the time the phase's tiles are done, and the next phase's first
+  // data load waits for nothing else (tile 0: loaded at the kernel start).
+  int4 sl_nx = sl0;
   auto run_phase = [&](auto PC) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
     const int t0 = tstart[P], t1 = tstart[P + 1];
     if (t0 >= t1) return;
     t_last = t1 - 1;
-    if (t0 > 0) fetch_slots(t0);  // tile 0's slots were loaded at the start
+    sl = sl_nx;
     fetch_data(PC, t0);
+    sl_nx = *reinterpret_cast<const int4*>(lh + (int64_t)min(t1, tstart[4] - 1) * BN + 4 * kg);
     fetch_slots(t0 + 1);
     decode_tile(PC, t0, buf);
     fetch_data(PC, t0 + 1);
