@@ -598,9 +598,11 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 
   // Tiles are processed in precision phases (the list regions): every load
   // and decode below is specialised for the phase's precision P, so no branch
-  // merges registers that still have loads in flight. Prefetches are
-  // unconditional: indices past the phase's last tile are clamped to it (a
-  // harmless re-read).
+  // inside a phase's tile loop merges registers that still have loads in
+  // flight (the compiler would then wait for them in every iteration). Within
+  // the loop prefetches are unconditional: indices past the phase's last tile
+  // are clamped to it (a harmless re-read). Only the peeled last tile of a
+  // phase branches, to load the next phase's first tile.
   int t_last = 0;  // last tile of the current phase
   auto fetch_slots = [&](int tt) __attribute__((always_inline)) {
     tt = min(tt, t_last);
@@ -834,23 +836,51 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   // landed by the time the phase's tiles are done, and the next phase's first
   // data load waits for nothing else (tile 0: loaded at the kernel start).
   int4 sl_nx = sl0;
+  // During a phase's last tile, the first tile of the next non-empty phase
+  // (precision Q > P, the phase starting at tile tstart[P + 1]) is loaded into
+  // rk / rv with Q's loads, so the next phase starts with its decode. The
+  // choice of Q is a wave-uniform branch; its loads are first read by that
+  // decode, which needs them anyway.
+  bool pref = false;  // rk / rv hold the first tile of the phase about to run
+  auto fetch_first = [&](auto QC) __attribute__((always_inline)) {
+    constexpr int Q = decltype(QC)::value;
+    t_last = tstart[Q + 1] - 1;
+    sl = sl_nx;
+    fetch_data(QC, tstart[Q]);
+    pref = true;
+  };
+  auto prefetch_next = [&](auto PC) __attribute__((always_inline)) {
+    constexpr int P = decltype(PC)::value;
+    if constexpr (P + 1 <= SI_PREC_INT4) {
+      if (tstart[P + 1] < tstart[P + 2]) {
+        fetch_first(std::integral_constant<int, P + 1>{});
+      } else if constexpr (P + 2 <= SI_PREC_INT4) {
+        if (tstart[P + 2] < tstart[P + 3]) {
+          fetch_first(std::integral_constant<int, P + 2>{});
+        } else if constexpr (P + 3 <= SI_PREC_INT4) {
+          if (tstart[P + 3] < tstart[P + 4]) fetch_first(std::integral_constant<int, P + 3>{});
+        }
+      }
+    }
+  };
   auto run_phase = [&](auto PC) __attribute__((always_inline)) {
     constexpr int P = decltype(PC)::value;
     const int t0 = tstart[P], t1 = tstart[P + 1];
     if (t0 >= t1) return;
     t_last = t1 - 1;
     sl = sl_nx;
-    fetch_data(PC, t0);
+    if (!pref) fetch_data(PC, t0);  // else loaded during the last phase's last tile
+    pref = false;
     sl_nx = *reinterpret_cast<const int4*>(lh + (int64_t)min(t1, tstart[4] - 1) * BN + 4 * kg);
     fetch_slots(t0 + 1);
     decode_tile(PC, t0, buf);
     fetch_data(PC, t0 + 1);
     fetch_slots(t0 + 2);
     lds_barrier();
-    for (int tt = t0; tt < t1; ++tt) {
+    // All tiles but the last; the loop body has no branch over loads in flight.
+    for (int tt = t0; tt < t1 - 1; ++tt) {
       compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(tt, P)), buf);
-      // Decode the next tile into the other buffer (after the phase's last
-      // tile: a clamped copy nobody reads), then prefetch.
+      // Decode the next tile into the other buffer, then prefetch.
       decode_tile(PC, min(tt + 1, t_last), buf ^ 1);
       fetch_data(PC, tt + 2);
       fetch_slots(tt + 3);
@@ -858,7 +888,11 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
       lds_barrier();
       buf ^= 1;
     }
-    // The phase's last decode (a clamped copy) went into buf; nothing reads it.
+    // The last tile; meanwhile the next phase's first tile is loaded.
+    compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(t_last, P)), buf);
+    prefetch_next(PC);
+    lds_barrier();  // also frees the tile buffers for the output staging
+    buf ^= 1;
   };
   run_phase(std::integral_constant<int, SI_PREC_FP32>{});
   run_phase(std::integral_constant<int, SI_PREC_FP16>{});
