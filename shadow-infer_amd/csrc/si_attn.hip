@@ -836,6 +836,17 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   // landed by the time the phase's tiles are done, and the next phase's first
   // data load waits for nothing else (tile 0: loaded at the kernel start).
   int4 sl_nx = sl0;
+  // Slots of the second tile of the next phase, clamped to that phase's last
+  // tile. For the first non-empty phase (it starts at tile 0 and ends before
+  // the first tstart[q] > 0): tile min(1, its last tile), loaded here.
+  int4 sl_n2;
+  {
+    const int fl = tstart[1] > 0 ? tstart[1] - 1
+                 : tstart[2] > 0 ? tstart[2] - 1
+                 : tstart[3] > 0 ? tstart[3] - 1
+                                 : max(tstart[4] - 1, 0);
+    sl_n2 = *reinterpret_cast<const int4*>(lh + (int64_t)min(1, fl) * BN + 4 * kg);
+  }
   // During a phase's last tile, the first tile of the next non-empty phase
   // (precision Q > P, the phase starting at tile tstart[P + 1]) is loaded into
   // rk / rv with Q's loads, so the next phase starts with its decode. The
@@ -872,7 +883,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     if (!pref) fetch_data(PC, t0);  // else loaded during the last phase's last tile
     pref = false;
     sl_nx = *reinterpret_cast<const int4*>(lh + (int64_t)min(t1, tstart[4] - 1) * BN + 4 * kg);
-    fetch_slots(t0 + 1);
+    sl = sl_n2;  // slots of tile min(t0 + 1, t_last), loaded before this phase
     decode_tile(PC, t0, buf);
     fetch_data(PC, t0 + 1);
     fetch_slots(t0 + 2);
@@ -888,7 +899,25 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
       lds_barrier();
       buf ^= 1;
     }
-    // The last tile; meanwhile the next phase's first tile is loaded.
+    // The last tile; meanwhile the next phase's first tile is loaded, and the
+    // slots of its second tile (clamped to that phase's last tile, nl).
+    {
+      // the next non-empty phase ends at the first tstart[q] > t1, q > P + 1
+      int nl = t1;
+      if constexpr (P + 2 <= 4) {
+        if (tstart[P + 2] > t1) {
+          nl = tstart[P + 2] - 1;
+        } else if constexpr (P + 3 <= 4) {
+          if (tstart[P + 3] > t1) {
+            nl = tstart[P + 3] - 1;
+          } else if constexpr (P + 4 <= 4) {
+            if (tstart[P + 4] > t1) nl = tstart[P + 4] - 1;
+          }
+        }
+      }
+      const int i2 = min(min(t1 + 1, nl), max(tstart[4] - 1, 0));
+      sl_n2 = *reinterpret_cast<const int4*>(lh + (int64_t)i2 * BN + 4 * kg);
+    }
     compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(t_last, P)), buf);
     prefetch_next(PC);
     lds_barrier();  // also frees the tile buffers for the output staging
