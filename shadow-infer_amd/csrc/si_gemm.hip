@@ -1011,19 +1011,27 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
       __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + 256 * ks), (lvoid_t*)(dst + 4096 * j),
                                        16, 0, 0);
   };
-  // this thread's outputs are e = threadIdx.x + 256 x: row e / nrows, column e % nrows
-  constexpr int EPT = MF * G;
+  // Outputs in 4-column pieces: item e = threadIdx.x + 256 x is activation row
+  // e / PPR and weight rows 4 (e % PPR) .. +3 of the block. With RB a multiple
+  // of 4 (the plan's choice) and ep.vec, a piece is one 16-byte (int32, fp32)
+  // or 8-byte (fp16, bf16) store; its scales are loaded here, before the
+  // first stage, so no load waits in the tail.
+  constexpr int PPR = 4 * G;
+  constexpr int IPT = (16 * MF * PPR + 255) / 256;
   const int mm = min(M, 16 * MF);
-  float esx[EPT], esw[EPT], eb[EPT];
+  const bool vec4 = ep.vec && RB % 4 == 0;
+  float esx[IPT];
+  float4 esw[IPT], eb[IPT];
 #pragma unroll
-  for (int x = 0; x < EPT; ++x) {
+  for (int x = 0; x < IPT; ++x) {
     const int e = threadIdx.x + 256 * x;
-    const int m = e / nrows, jj = e - m * nrows;
-    esx[x] = esw[x] = eb[x] = 0.0f;
-    if (EPI == EPI_DEQUANT && m < mm) {
+    const int m = e / PPR, j0 = 4 * (e - m * PPR);
+    esx[x] = 0.0f;
+    esw[x] = eb[x] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (EPI == EPI_DEQUANT && m < mm && vec4 && j0 + 4 <= nrows) {
       esx[x] = ep.sx[m];
-      esw[x] = ep.sw[n0 + jj];
-      if (ep.bias != nullptr) eb[x] = ep.bias[n0 + jj];
+      esw[x] = *reinterpret_cast<const float4*>(ep.sw + n0 + j0);
+      if (ep.bias != nullptr) eb[x] = *reinterpret_cast<const float4*>(ep.bias + n0 + j0);
     }
   }
 #pragma unroll
@@ -1071,21 +1079,55 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
         red[w * PART + (16 * g + fr) * RP + 16 * i + 4 * fc + r] = acc[g][i][r];
   __syncthreads();
 #pragma unroll
-  for (int x = 0; x < EPT; ++x) {
+  for (int x = 0; x < IPT; ++x) {
     const int e = threadIdx.x + 256 * x;
-    const int m = e / nrows, jj = e - m * nrows;
-    if (m < mm) {
-      int32_t v = 0;
+    const int m = e / PPR, j0 = 4 * (e - m * PPR);
+    if (m >= mm || j0 >= nrows) continue;
+    int32_t v[4];
 #pragma unroll
-      for (int y = 0; y < 4; ++y) v += red[y * PART + jj * RP + m];
-      if (EPI == EPI_DEQUANT) {
-        float o = (float)v * (esx[x] * esw[x]);
-        if (ep.bias != nullptr) o = o + eb[x];
-        const int64_t idx = (int64_t)m * N + n0 + jj;
-        store_any(ep.out, ep.out_dtype, idx, add_resid_rt(ep, idx, o));
-      } else {
-        epi_store<EPI>(ep, C, M, N, m, n0 + jj, v, 0);
+    for (int j = 0; j < 4; ++j) {
+      v[j] = 0;
+#pragma unroll
+      for (int y = 0; y < 4; ++y) v[j] += red[y * PART + (j0 + j) * RP + m];
+    }
+    const int64_t idx = (int64_t)m * N + n0 + j0;
+    if (!vec4 || j0 + 4 > nrows) {  // ragged last piece or unaligned operands
+      for (int j = 0; j < 4 && j0 + j < nrows; ++j) epi_store<EPI>(ep, C, M, N, m, n0 + j0 + j, v[j], 0);
+      continue;
+    }
+    if (EPI != EPI_DEQUANT) {
+      *reinterpret_cast<v4i*>(C + idx) = v4i{v[0], v[1], v[2], v[3]};
+      continue;
+    }
+    const float w[4] = {esw[x].x, esw[x].y, esw[x].z, esw[x].w};
+    const float bb[4] = {eb[x].x, eb[x].y, eb[x].z, eb[x].w};
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[j] = (float)v[j] * (esx[x] * w[j]);
+      if (ep.bias != nullptr) o[j] = o[j] + bb[j];
+    }
+    if (ep.out_dtype == SI_DT_F32) {
+      float* out = reinterpret_cast<float*>(ep.out) + idx;
+      if (ep.resid != nullptr) {
+        const float4 r = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ep.resid) + idx);
+        o[0] += r.x; o[1] += r.y; o[2] += r.z; o[3] += r.w;
       }
+      *reinterpret_cast<float4*>(out) = make_float4(o[0], o[1], o[2], o[3]);
+    } else {
+      const bool f16 = ep.out_dtype == SI_DT_F16;
+      if (ep.resid != nullptr) {
+        const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(ep.resid) + idx);
+        const uint32_t rh[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = round_to(o[j], ep.out_dtype) + (f16 ? f16_bits_to_f32(rh[j]) : bf16_bits_to_f32(rh[j]));
+      }
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = f16 ? f32_to_f16_bits(o[j]) : f32_to_bf16_bits(o[j]);
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(ep.out) + idx) =
+          make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     }
   }
 }
@@ -1206,11 +1248,15 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
   const int64_t rows_per_cu = ceil_div(N, 256);
   if (forced_kind() >= 0) {
     kind = forced_kind();
-  } else if (M <= 32 && K % 256 == 0 && rows_per_cu >= 16 && rows_per_cu <= 48) {
+  } else if (K % 256 == 0 && rows_per_cu >= 16 && rows_per_cu <= 48 &&
+             (M <= 32 || (M <= 128 && rows_per_cu >= 17))) {
     // Each CU streams its own ceil(N / 256) weight rows once: 11008 x 4096 at
     // M = 16 / 32: 14.1 / 14.7 -> 10.2 / 11.3 us; 4096 x 11008: 14.0 / 15.0 ->
-    // 13.6 / 14.5 us. From 33 rows the activation copies outweigh the weight's
-    // and the tile kernels are as fast.
+    // 13.6 / 14.5 us. With 17-48 rows per CU this beats the 64-row tiles up to
+    // M = 128 (4096 -> 11008 at M = 40 / 64 / 96 / 128: 13.5 / 14.5 / 17.2 /
+    // 18.9 -> 11.1 / 13.2 / 16.1 / 18.7 us; 4096 -> 8192 at M = 64: 11.4 -> 9.6
+    // us); with 16 rows per CU (N = 4096) the activation rows outweigh the
+    // weight's from M = 33 (M = 96: 18.5 against 23.7 us for the tiles).
     kind = K_ROWS;
   } else if (K % 128 == 0 && M <= 128 &&
              (M > 16 || (M > 8 && ceil_div(N, 64) >= 128 && ceil_div(N, 64) < 256))) {
@@ -1260,10 +1306,10 @@ Plan choose(int64_t M, int64_t N, int64_t K) {
     kind = K_TILE_128x128;
   }
   if (kind == K_ROWS) {
-    if (M <= 32 && K % 256 == 0 && rows_per_cu <= 48) {
+    if (K % 256 == 0 && rows_per_cu <= 48 && (M <= 32 || (M <= 128 && rows_per_cu >= 17))) {
       p.kind = K_ROWS;
-      p.mf = M <= 16 ? 1 : 2;
-      p.bn = (int)rows_per_cu;
+      p.mf = (int)ceil_div(M, 16);
+      p.bn = (int)(ceil_div(rows_per_cu, 4) * 4);  // whole 4-column output pieces per block
       return p;
     }
     kind = K_TILE_128x128;
@@ -1411,10 +1457,19 @@ void launch_rows(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, 
   const int G = (p.bn + 15) / 16;
   // 16-row stages are small (8-12 KB): six of them keep about as many bytes in
   // flight as four of the 48-row stages (16 x 4096 x 11008: 12.9 -> 11.8 us,
-  // 32 rows 13.6 -> 13.1 us)
-  if (G == 1) gemm_rows<MF, 1, 6, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
-  else if (G == 2) gemm_rows<MF, 2, 4, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
-  else gemm_rows<MF, 3, 4, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+  // 32 rows 13.6 -> 13.1 us). 16 weight rows per CU only up to 32 activation
+  // rows (choose); wider stages take four slots, or three where four would not
+  // fit in 160 KB of LDS.
+  if constexpr (MF <= 2) {
+    if (G == 1) {
+      gemm_rows<MF, 1, 6, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+      return;
+    }
+  }
+  constexpr int R2 = 16 * (2 + MF) * 256 * 4 <= 160 * 1024 ? 4 : 3;
+  constexpr int R3 = 16 * (3 + MF) * 256 * 4 <= 160 * 1024 ? 4 : 3;
+  if (G <= 2) gemm_rows<MF, 2, R2, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
+  else gemm_rows<MF, 3, R3, EPI><<<grid, 256, 0, st>>>(a, b, M, N, K, p.bn, c, ep);
 }
 
 template <int EPI>
@@ -1422,8 +1477,16 @@ void launch(const Plan& p, const int8_t* a, const int8_t* b, int M, int N, int K
             const EpiArgs& ep, hipStream_t st) {
   const dim3 block(256);
   if (p.kind == K_ROWS) {
-    if (p.mf == 1) launch_rows<1, EPI>(p, a, b, M, N, K, c, ep, st);
-    else launch_rows<2, EPI>(p, a, b, M, N, K, c, ep, st);
+    switch (p.mf) {
+      case 1: launch_rows<1, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 2: launch_rows<2, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 3: launch_rows<3, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 4: launch_rows<4, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 5: launch_rows<5, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 6: launch_rows<6, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      case 7: launch_rows<7, EPI>(p, a, b, M, N, K, c, ep, st); break;
+      default: launch_rows<8, EPI>(p, a, b, M, N, K, c, ep, st);
+    }
     return;
   }
   if (p.kind == K_STREAM_N64 || p.kind == K_STREAM_N64_W8 || p.kind == K_STREAM_N32 ||

@@ -72,13 +72,17 @@ def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
                                    (24, 4096, 11008), (48, 11008, 4096), (128, 4096, 11008),
                                    (128, 11008, 4096), (40, 4096, 22016), (100, 4096, 1000),
                                    (256, 11008, 4096), (384, 11008, 4096), (200, 4096, 3000),
-                                   (129, 4096, 11008), (200, 4096, 11000), (256, 4096, 12288)])
+                                   (129, 4096, 11008), (200, 4096, 11000), (256, 4096, 12288),
+                                   # row streaming with 3..8 16-row activation fragments
+                                   (33, 4096, 11008), (80, 4096, 8192), (100, 4096, 6000),
+                                   (112, 4096, 12288), (96, 1280, 11008), (48, 1024, 5000)])
 def test_gemm_i32_large_m_exact(dev, M, K, N):
     """FFN shapes (up, fused gate|up and down) against the exact float64 product:
     large M on the 256-row tiles, 129..256 rows of the up projection on the
     128x96 tiles (ragged rows and columns included), 17..128 rows on the
-    64x64 / 64x128 / 128x128 tiles with and without split K, and the down
-    projection split in K up to 512 rows."""
+    64x64 / 64x128 / 128x128 tiles with and without split K or streamed per CU
+    over 17-48 weight rows (ragged last blocks, three or four LDS stages), and
+    the down projection split in K up to 512 rows."""
     g = torch.Generator().manual_seed(M + K)
     a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
     b = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(dev)
@@ -351,7 +355,8 @@ def test_int4_all_nibble_pairs(dev):
 @pytest.mark.parametrize("M,K,N,bias", [(16, 4096, 11008, False), (8, 320, 3000, True),
                                         (64, 4096, 11008, False), (48, 11008, 4096, True),
                                         (300, 512, 272, True), (5, 40, 24, False),
-                                        (128, 4000, 300, False), (200, 128, 9600, True)])
+                                        (128, 4000, 300, False), (200, 128, 9600, True),
+                                        (100, 4096, 6000, True)])
 def test_gemm_dequant_add_bit_exact(dev, dtype, M, K, N, bias):
     """si_gemm_i8_dequant_add = T(residual + T(acc * (sx * sw) [+ bias])), the
     INT8Linear output rounded to T and added to the residual stream in T
