@@ -481,26 +481,33 @@ def bench_gemm(torch, dev, iters=50):
         _native.call("si_act_quant_i8", x.data_ptr(), _native.DT_BF16, M, K, q.data_ptr(),
                      sx.data_ptr(), sptr)
         it = [0]
+        # The library entry points are bound once and their arguments built
+        # before the timed loops: at 10-15 us per launch, Python-side argument
+        # marshalling per call would otherwise set the pace instead of the GPU.
+        lib = _native.load()
+        f_gemm, f_fwd, f_deq = lib.si_gemm_i8i8_i32, lib.si_int8_linear_forward, lib.si_gemm_i8_dequant
+        a_gemm = [(q.data_ptr(), w.data_ptr(), M, N, K, c.data_ptr(), gws.data_ptr(), gws_b, sptr)
+                  for w in ws]
+        a_fwd = [(x.data_ptr(), _native.DT_BF16, M, K, N, w.data_ptr(), sw.data_ptr(), None,
+                  y.data_ptr(), lws.data_ptr(), lws_b, sptr) for w in ws]
+        a_deq = [(q.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(), None, M, N, K,
+                  y.data_ptr(), _native.DT_BF16, gws.data_ptr(), gws_b, sptr) for w in ws]
+        rcs = []
 
         def gemm():
-            w = ws[it[0] % copies]
+            i = it[0] % copies
             it[0] += 1
-            _native.call("si_gemm_i8i8_i32", q.data_ptr(), w.data_ptr(), M, N, K, c.data_ptr(),
-                         gws.data_ptr(), gws_b, sptr)
+            rcs.append(f_gemm(*a_gemm[i]))
 
         def forward():
-            w = ws[it[0] % copies]
+            i = it[0] % copies
             it[0] += 1
-            _native.call("si_int8_linear_forward", x.data_ptr(), _native.DT_BF16, M, K, N,
-                         w.data_ptr(), sw.data_ptr(), None, y.data_ptr(), lws.data_ptr(), lws_b,
-                         sptr)
+            rcs.append(f_fwd(*a_fwd[i]))
 
         def gemm_dequant():  # the GEMM with INT8Linear's epilogue, bf16 out
-            w = ws[it[0] % copies]
+            i = it[0] % copies
             it[0] += 1
-            _native.call("si_gemm_i8_dequant", q.data_ptr(), sx.data_ptr(), w.data_ptr(),
-                         sw.data_ptr(), None, M, N, K, y.data_ptr(), _native.DT_BF16,
-                         gws.data_ptr(), gws_b, sptr)
+            rcs.append(f_deq(*a_deq[i]))
 
         for _ in range(5):
             gemm()
@@ -509,6 +516,8 @@ def bench_gemm(torch, dev, iters=50):
         ms_gemm = timer.time(gemm, iters)
         ms_deq = timer.time(gemm_dequant, iters)
         ms_fwd = timer.time(forward, iters)
+        if any(rc != 0 for rc in rcs):
+            raise RuntimeError(f"INT8 GEMM launch failed: {lib.si_last_error().decode(errors='replace')}")
         ops = 2.0 * M * K * N
         # The vendor library on the same operands: hipBLASLt through
         # torch._int_mm (it needs more than 16 rows), weight as the [K, N]
