@@ -959,9 +959,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_stream(const int8_t* __restrict_
 // (row runs of 256 B keep the HBM bursts whole, where the 64-byte row pieces
 // of direct fragment loads do not), chunk p of row r stored at slot p ^ (r &
 // 15) so that the 16 rows of one fragment read fall on distinct banks. R
-// stages rotate with one barrier per stage; wave w multiplies k step w of each
-// stage for all G row groups, and the four waves' partial sums over disjoint
-// k are added in LDS at the end. Blocks start their k loop at different
+// stages rotate with one barrier per stage; wave w multiplies activation
+// fragments w, w + 4, .. against all G weight groups over the whole stage, and
+// the finished sums go through LDS once, for row-contiguous stores. Blocks
+// start their k loop at different
 // stages (the int32 sums do not depend on the order), which spreads the CUs
 // of one XCD over different activation lines. The epilogue's scales are
 // loaded before the first stage, so no load waits in the tail.
@@ -1038,45 +1039,100 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
   for (int u = 0; u < R - 1; ++u)
     if (u < stages) issue(u, u);
   const int fr = lane & 15, fc = lane >> 4;
-  const int foff = 256 * fr + 16 * ((4 * w + fc) ^ fr);  // k step w of a 16-row group
-  v4i acc[G][MF];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < MF; ++i) acc[g][i] = v4i{0, 0, 0, 0};
+  // The block's sums go through LDS for the row-contiguous stores below. Two
+  // ways to split the MFMAs over the four waves:
+  // - MF a multiple of 4: wave w owns activation fragments w, w + 4, .. against
+  //   every weight group over all four 64-byte k-steps of each stage, so no
+  //   partial sums cross waves and the finished sums go to LDS as
+  //   [activation row][weight row], pitch TP words (M = 64: 13.0 -> 12.5 us,
+  //   M = 128: 18.0 -> 16.6 us against the k-step split);
+  // - otherwise wave w multiplies k-step w of each stage for every fragment,
+  //   and the four waves' partial sums are added in LDS (with fewer than four
+  //   fragments the other split would leave waves idle and run each stage's
+  //   MFMAs as one wave's dependent chain: M = 16 9.5 -> 21 us).
+  constexpr int TP = 16 * G + 4;       // tile pitch (words)
+  constexpr int RP = 16 * MF + 4;      // partial-sum pitch (words)
+  constexpr int PART = 16 * G * RP;    // one wave's partial sums
+  int32_t* const red = reinterpret_cast<int32_t*>(lds);  // the tile, or the four partials
   int slot = 0;
-  for (int s = 0; s < stages; ++s) {
-    wait_stages<IPW, R - 2>(stages - 1 - s);  // stages s+1 .. s+R-2 may stay in flight
-    bare_barrier();                            // every wave's copies of stage s landed;
-    if (s + R - 1 < stages)                    // every wave is done with stage s-1
-      issue(s + R - 1, slot == 0 ? R - 1 : slot - 1);
-    const int8_t* base = lds + slot * STAGE + foff;
-    v4i a[MF], b[G];
+  if constexpr (MF % 4 == 0) {
+    static_assert(16 * MF * TP * 4 <= R * STAGE, "output tile fits in the stages");
+    constexpr int IW = MF / 4;
+    v4i acc[G][IW];
 #pragma unroll
-    for (int i = 0; i < MF; ++i) a[i] = *reinterpret_cast<const v4i*>(base + 4096 * (G + i));
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int g = 0; g < G; ++g) b[g] = *reinterpret_cast<const v4i*>(base + 4096 * g);
+      for (int j = 0; j < IW; ++j) acc[g][j] = v4i{0, 0, 0, 0};
+    for (int s = 0; s < stages; ++s) {
+      wait_stages<IPW, R - 2>(stages - 1 - s);  // stages s+1 .. s+R-2 may stay in flight
+      bare_barrier();                            // every wave's copies of stage s landed;
+      if (s + R - 1 < stages)                    // every wave is done with stage s-1
+        issue(s + R - 1, slot == 0 ? R - 1 : slot - 1);
+      const int8_t* sb = lds + slot * STAGE + 256 * fr;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int8_t* base = sb + 16 * ((4 * ks + fc) ^ fr);  // k step ks of a 16-row group
+        v4i a[IW], b[G];
+#pragma unroll
+        for (int j = 0; j < IW; ++j) a[j] = *reinterpret_cast<const v4i*>(base + 4096 * (G + w + 4 * j));
+#pragma unroll
+        for (int g = 0; g < G; ++g) b[g] = *reinterpret_cast<const v4i*>(base + 4096 * g);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int j = 0; j < IW; ++j)
+            acc[g][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[j], b[g], acc[g][j], 0, 0, 0);
+      }
+      slot = slot == R - 1 ? 0 : slot + 1;
+    }
+    __syncthreads();
+    // accumulator register r of (g, j): activation row 16 (w + 4j) + 4 (lane / 16)
+    // + r, weight row 16g + lane % 16
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < IW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          red[(16 * (w + 4 * j) + 4 * fc + r) * TP + 16 * g + fr] = acc[g][j][r];
+  } else {
+    const int foff = 256 * fr + 16 * ((4 * w + fc) ^ fr);  // k step w of a 16-row group
+    v4i acc[G][MF];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < MF; ++i) acc[g][i] = v4i{0, 0, 0, 0};
+    for (int s = 0; s < stages; ++s) {
+      wait_stages<IPW, R - 2>(stages - 1 - s);  // stages s+1 .. s+R-2 may stay in flight
+      bare_barrier();                            // every wave's copies of stage s landed;
+      if (s + R - 1 < stages)                    // every wave is done with stage s-1
+        issue(s + R - 1, slot == 0 ? R - 1 : slot - 1);
+      const int8_t* base = lds + slot * STAGE + foff;
+      v4i a[MF], b[G];
+#pragma unroll
+      for (int i = 0; i < MF; ++i) a[i] = *reinterpret_cast<const v4i*>(base + 4096 * (G + i));
+#pragma unroll
+      for (int g = 0; g < G; ++g) b[g] = *reinterpret_cast<const v4i*>(base + 4096 * g);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+          acc[g][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[g], acc[g][i], 0, 0, 0);
+      slot = slot == R - 1 ? 0 : slot + 1;
+    }
+    __syncthreads();
+    // accumulator register r of (g, i): activation row 16i + 4(lane/16) + r,
+    // weight row 16g + lane%16; wave w's partial sums at red + w * PART, added
+    // by the stores below
+    static_assert(4 * PART * 4 <= R * STAGE, "reduction area");
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int i = 0; i < MF; ++i)
-        acc[g][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[g], acc[g][i], 0, 0, 0);
-    slot = slot == R - 1 ? 0 : slot + 1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          red[w * PART + (16 * g + fr) * RP + 16 * i + 4 * fc + r] = acc[g][i][r];
   }
-  __syncthreads();
-  // accumulator register r of (g, i): activation row 16i + 4(lane/16) + r,
-  // weight row 16g + lane%16
-  constexpr int RP = 16 * MF + 4;
-  constexpr int PART = 16 * G * RP;
-  static_assert(4 * PART * 4 <= R * STAGE, "reduction area");
-  int32_t* red = reinterpret_cast<int32_t*>(lds);
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < MF; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        red[w * PART + (16 * g + fr) * RP + 16 * i + 4 * fc + r] = acc[g][i][r];
   __syncthreads();
 #pragma unroll
   for (int x = 0; x < IPT; ++x) {
@@ -1084,11 +1140,17 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
     const int m = e / PPR, j0 = 4 * (e - m * PPR);
     if (m >= mm || j0 >= nrows) continue;
     int32_t v[4];
+    if constexpr (MF % 4 == 0) {
+      const v4i tv = *reinterpret_cast<const v4i*>(red + m * TP + j0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[j] = 0;
+      for (int j = 0; j < 4; ++j) v[j] = tv[j];
+    } else {
 #pragma unroll
-      for (int y = 0; y < 4; ++y) v[j] += red[y * PART + (j0 + j) * RP + m];
+      for (int j = 0; j < 4; ++j) {
+        v[j] = 0;
+#pragma unroll
+        for (int y = 0; y < 4; ++y) v[j] += red[y * PART + (j0 + j) * RP + m];
+      }
     }
     const int64_t idx = (int64_t)m * N + n0 + j0;
     if (!vec4 || j0 + 4 > nrows) {  // ragged last piece or unaligned operands
