@@ -75,7 +75,8 @@ def test_gemm_i32_bit_exact_vs_oracle(dev, M, K, N):
                                    (129, 4096, 11008), (200, 4096, 11000), (256, 4096, 12288),
                                    # row streaming with 3..8 16-row activation fragments
                                    (33, 4096, 11008), (80, 4096, 8192), (100, 4096, 6000),
-                                   (112, 4096, 12288), (96, 1280, 11008), (48, 1024, 5000)])
+                                   (112, 4096, 12288), (96, 1280, 11008), (48, 1024, 5000),
+                                   (64, 512, 5001), (128, 768, 4099), (61, 256, 8190)])
 def test_gemm_i32_large_m_exact(dev, M, K, N):
     """FFN shapes (up, fused gate|up and down) against the exact float64 product:
     large M on the 256-row tiles, 129..256 rows of the up projection on the
@@ -356,7 +357,8 @@ def test_int4_all_nibble_pairs(dev):
                                         (64, 4096, 11008, False), (48, 11008, 4096, True),
                                         (300, 512, 272, True), (5, 40, 24, False),
                                         (128, 4000, 300, False), (200, 128, 9600, True),
-                                        (100, 4096, 6000, True)])
+                                        (100, 4096, 6000, True), (64, 512, 5001, True),
+                                        (128, 768, 4100, False)])
 def test_gemm_dequant_add_bit_exact(dev, dtype, M, K, N, bias):
     """si_gemm_i8_dequant_add = T(residual + T(acc * (sx * sw) [+ bias])), the
     INT8Linear output rounded to T and added to the residual stream in T
