@@ -109,6 +109,19 @@ __device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float v) {
   }
 }
 
+// A pointer that is the same in every lane, read from lane 0 so that code
+// built on it (a buffer descriptor) stays in scalar registers; the compiler
+// cannot always prove such values uniform (a wave index from threadIdx.x), and
+// a descriptor in vector registers costs a waterfall loop around every use.
+// readfirstlane returns an int: each half goes through uint32_t, or a low
+// half with bit 31 set would sign-extend over the high half.
+__device__ __forceinline__ void* wave_uniform(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  return reinterpret_cast<void*>(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
 // Round an fp32 value to dtype dt and widen back (identity for fp32).
 __device__ __forceinline__ float round_to(float v, int dt) {
   if (dt == SI_DT_F32) return v;

@@ -384,7 +384,7 @@ __device__ __forceinline__ void load8_out(const void* p, int64_t idx, float* r) 
 // first row); offsets within a band stay below 2^32 because N * K < 2^31 and
 // K >= 64.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t band_rsrc(void* band) {
-  return __builtin_amdgcn_make_buffer_rsrc(band, (short)0, -1, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(wave_uniform(band), (short)0, -1, 0x00020000);
 }
 
 // 16 bytes at byte `off` of a band, stored with device scope (sc1): the lines

@@ -422,8 +422,8 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 // Raw buffer from byte `first` of a bucket (block-uniform); `off` is the
 // byte offset from there (a block's rows span a few KB).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(void* bucket, int64_t first) {
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(bucket) + first, (short)0, -1,
-                                           0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(wave_uniform(reinterpret_cast<char*>(bucket) + first),
+                                           (short)0, -1, 0x00020000);
 }
 __device__ __forceinline__ void st_dev(void* bucket, int64_t first, uint32_t off, u32x4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, rows_rsrc(bucket, first), (int)off, 0, 16);
