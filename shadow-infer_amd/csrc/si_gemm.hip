@@ -1157,8 +1157,9 @@ __global__ __launch_bounds__(256) void gemm_rows(const int8_t* __restrict__ A,
       for (int j = 0; j < 4 && j0 + j < nrows; ++j) epi_store<EPI>(ep, C, M, N, m, n0 + j0 + j, v[j], 0);
       continue;
     }
-    if (EPI != EPI_DEQUANT) {
-      *reinterpret_cast<v4i*>(C + idx) = v4i{v[0], v[1], v[2], v[3]};
+    if (EPI != EPI_DEQUANT) {  // device scope, as in the tiles' int32 epilogue (M = 128: 16.5 -> 15.8 us)
+      store16_dev(band_rsrc(C + n0), ((uint32_t)m * (uint32_t)N + (uint32_t)j0) * 4u,
+                  v4i{v[0], v[1], v[2], v[3]});
       continue;
     }
     const float w[4] = {esw[x].x, esw[x].y, esw[x].z, esw[x].w};
