@@ -1598,7 +1598,10 @@ int run_gemm(const int8_t* a, const int8_t* b, int64_t M, int64_t N, int64_t K, 
     uintptr_t bits = reinterpret_cast<uintptr_t>(c) | reinterpret_cast<uintptr_t>(ep.out) |
                      reinterpret_cast<uintptr_t>(ep.sw) | reinterpret_cast<uintptr_t>(ep.bias) |
                      reinterpret_cast<uintptr_t>(ep.resid) | reinterpret_cast<uintptr_t>(ws);
-    ep.vec = (N % 8 == 0 && (bits & 15) == 0) ? 1 : 0;
+    // The int32 epilogues' device-scope buffer stores address a band of at
+    // most 128 output rows by a 32-bit byte offset (< 512 N): wider outputs
+    // take the per-element stores.
+    ep.vec = (N % 8 == 0 && (bits & 15) == 0 && N < ((int64_t)1 << 22)) ? 1 : 0;
   }
   if (p.kind == K_SCALAR) {
     const int64_t blocks = std::min<int64_t>(ceil_div(M * N, 256), 65536);

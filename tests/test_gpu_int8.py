@@ -91,6 +91,26 @@ def test_gemm_i32_large_m_exact(dev, M, K, N):
     assert torch.equal(c.to(torch.int64), _exact_i32(a, b))
 
 
+@pytest.mark.parametrize("N", [(1 << 22) - 8, (1 << 22) + 8])
+def test_gemm_i32_wide_output(dev, N):
+    """Output rows of 4M columns, just below and just above the width where the
+    int32 epilogue leaves its 32-bit-offset buffer stores for per-element ones:
+    sampled columns (both ends and a random set) against the exact product."""
+    M, K = 33, 128
+    g = torch.Generator(device=dev).manual_seed(N)
+    a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)  # [N, K]
+    c = torch.empty(M, N, dtype=torch.int32, device=dev)
+    ws_bytes = _native.size_query("si_gemm_workspace_bytes", M, N, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _native.call("si_gemm_i8i8_i32", a.data_ptr(), w.data_ptr(), M, N, K, c.data_ptr(),
+                 ws.data_ptr(), ws_bytes, _native.stream(dev))
+    cols = torch.cat([torch.arange(0, 512, device=dev), torch.arange(N - 512, N, device=dev),
+                      torch.randint(0, N, (4096,), generator=g, device=dev)])
+    want = (a.double() @ w[cols].double().t()).to(torch.int64)
+    assert torch.equal(c[:, cols].to(torch.int64), want)
+
+
 def test_gemm_extreme_values_no_overflow(dev):
     """All -127 x -127 over K=4096: the largest accumulator the layer can produce."""
     a = torch.full((16, 4096), -127, dtype=torch.int8, device=dev)
