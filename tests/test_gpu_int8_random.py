@@ -1,9 +1,9 @@
 """Seeded random shapes through every INT8 GEMM path the tile choice can take
 (weight streaming at several column widths, split K, 64x64 / 64x128 / 128x128 / 256x128 /
 256x192 / 256x256 tiles, the register-staged tile for K not a multiple of 64,
-the scalar kernel for K not a multiple of 16): int32 results against the exact
-float64 product, and the INT8Linear epilogue (int8_linear.py:102-115) against
-the oracle bit for bit."""
+the scalar kernel for K not a multiple of 16, the row-streaming kernel):
+int32 results against the exact float64 product, and the INT8Linear epilogue
+(int8_linear.py:102-115) against the oracle bit for bit."""
 
 import numpy as np
 import pytest
@@ -73,3 +73,30 @@ def test_random_dequant_epilogue_vs_oracle(dev, seed):
         got = out.cpu()
         got = got.view(torch.int16).numpy().view(np.uint16) if dt == torch.bfloat16 else got.numpy()
         np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+def test_random_row_stream_exact(dev, seed):
+    """Shapes of the row-streaming kernel (K a multiple of 256, 16-48 weight
+    rows per CU, up to 128 activation rows, ragged last blocks): int32 against
+    the exact product, and the bf16 / fp32 epilogues against the oracle's
+    epilogue over that product."""
+    rng = np.random.default_rng(500 + seed)
+    M, N, K = int(rng.integers(1, 129)), int(rng.integers(3841, 12289)), 256 * int(rng.integers(1, 44))
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    want = (a.double() @ b.double().t()).to(torch.int64)
+    assert torch.equal(_gemm(a, b, "i32").to(torch.int64), want), (M, N, K)
+    sx = torch.rand(M, generator=g, device=dev) * 0.05 + 1e-4
+    sw = torch.rand(N, generator=g, device=dev) * 0.01 + 1e-5
+    bias = torch.randn(N, generator=g, device=dev) if seed % 2 else None
+    acc = want.to(torch.int32).cpu().numpy()
+    for dt in (torch.bfloat16, torch.float32):
+        got = _gemm(a, b, "dequant", sx, sw, bias, dt).cpu()
+        ref = O.int8_epilogue(acc, sx.cpu().numpy(), sw.cpu().numpy(),
+                              None if bias is None else bias.cpu().numpy(),
+                              O.BF16 if dt == torch.bfloat16 else O.F32)
+        got = got.view(torch.int16).numpy().view(np.uint16) if dt == torch.bfloat16 else got.numpy()
+        np.testing.assert_array_equal(got, ref)
