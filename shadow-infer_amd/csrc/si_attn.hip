@@ -297,6 +297,24 @@ __device__ __forceinline__ void tile_qk(const _Float16 (*Ks)[D + KPAD], const v8
   }
 }
 
+// tile_qk_lo: S^T += Klo Q^T for caches of fp32 inputs, whose K values are
+// held as an fp16 pair hi + lo (hi = fp16(x), lo = fp16(x - hi)): the scores
+// then carry K to about 22 bits instead of fp16's 11. With fp32 K/V holding
+// outlier channels, K's fp16 rounding is most of the output's error (a model
+// of the kernel's roundings: relL2 8.8e-4 with it, 4.4e-4 without).
+template <int D>
+__device__ __forceinline__ void tile_qk_lo(const _Float16 (*Kl)[D + KPAD], const v8h* qf, int col,
+                                           int grp, v16f (&sacc)[2]) {
+  constexpr int KS = D / 16;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const v8h a0 = *reinterpret_cast<const v8h*>(&Kl[col][ks * 16 + 8 * grp]);
+    const v8h a1 = *reinterpret_cast<const v8h*>(&Kl[32 + col][ks * 16 + 8 * grp]);
+    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[ks], sacc[0], 0, 0, 0);
+    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[ks], sacc[1], 0, 0, 0);
+  }
+}
+
 // tile_softmax: online softmax of one tile's shifted scores in the log2 domain
 // (Q carries sm_scale * log2(e)). Keys at or past nv are masked. The running
 // max is raised only when a score exceeds it by more than 8 (a factor 2^8),
@@ -556,6 +574,9 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   // Two tile buffers: tile t+1 is decoded into one while tile t is multiplied from the other.
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][BN][D + KPAD];
   __shared__ __attribute__((aligned(16))) _Float16 Vs[2][BN][VR];
+  // fp32 inputs (fp32 scales): the low fp16 parts of K (tile_qk_lo)
+  constexpr bool KLO = SDT == SI_DT_F32;
+  __shared__ __attribute__((aligned(16))) _Float16 Kls[KLO ? 2 : 1][KLO ? BN : 1][D + KPAD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -714,8 +735,9 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         sk[i] = scale_from_bits<SDT>(skb[i]);
         sv[i] = scale_from_bits<SDT>(svb[i]);
       }
-      // Per key i: fp16 pair words of K (kw) and V (vw), dims (2x, 2x+1).
-      uint32_t kw[4][RW], vw[4][RW];
+      // Per key i: fp16 pair words of K (kw) and V (vw), dims (2x, 2x+1);
+      // with KLO also the low parts of K (kl).
+      uint32_t kw[4][RW], vw[4][RW], kl[4][RW];
       if constexpr (P == SI_PREC_FP16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -760,13 +782,27 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
         for (int i = 0; i < 4; ++i)
           fast &= (int)h_exact<SDT, P == SI_PREC_INT8>(skb[i], sk[i]) &
                   (int)h_exact<SDT, P == SI_PREC_INT8>(svb[i], sv[i]);
+        if constexpr (KLO) {
+          // K as the fp32 product float(q) * s (the unpack's value) split into
+          // fp16 hi + lo; V rounded once to fp16 as below.
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int x = 0; x < RW; ++x) {
+              const h2 a = as_h2(kw[i][x]);
+              const float p0 = (float)a[0] * sk[i], p1 = (float)a[1] * sk[i];
+              const _Float16 h0 = (_Float16)p0, h1 = (_Float16)p1;
+              kw[i][x] = pack_h2(h0, h1);
+              kl[i][x] = pack_h2((_Float16)(p0 - (float)h0), (_Float16)(p1 - (float)h1));
+            }
+        }
         if (__builtin_amdgcn_ballot_w64(fast == 0) == 0) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const h2 k2 = scale_h2<SDT>(skb[i], sk[i]), v2 = scale_h2<SDT>(svb[i], sv[i]);
 #pragma unroll
             for (int x = 0; x < RW; ++x) {
-              kw[i][x] = as_u32(as_h2(kw[i][x]) * k2);
+              if constexpr (!KLO) kw[i][x] = as_u32(as_h2(kw[i][x]) * k2);
               vw[i][x] = as_u32(as_h2(vw[i][x]) * v2);
             }
           }
@@ -776,7 +812,8 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
 #pragma unroll
             for (int x = 0; x < RW; ++x) {
               const h2 a = as_h2(kw[i][x]), c = as_h2(vw[i][x]);
-              kw[i][x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
+              if constexpr (!KLO)
+                kw[i][x] = pack_h2((_Float16)((float)a[0] * sk[i]), (_Float16)((float)a[1] * sk[i]));
               vw[i][x] = pack_h2((_Float16)((float)c[0] * sv[i]), (_Float16)((float)c[1] * sv[i]));
             }
         }
@@ -799,7 +836,10 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
           }
 #pragma unroll
           for (int x = 0; x < RW; ++x) {
-            kw[i][x] = pack_h2((_Float16)kx[2 * x], (_Float16)kx[2 * x + 1]);
+            const _Float16 h0 = (_Float16)kx[2 * x], h1 = (_Float16)kx[2 * x + 1];
+            kw[i][x] = pack_h2(h0, h1);
+            if constexpr (KLO)
+              kl[i][x] = pack_h2((_Float16)(kx[2 * x] - (float)h0), (_Float16)(kx[2 * x + 1] - (float)h1));
             vw[i][x] = pack_h2((_Float16)vx[2 * x], (_Float16)vx[2 * x + 1]);
           }
         }
@@ -813,6 +853,19 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
           *reinterpret_cast<uint2*>(&Ks[buf][4 * kg + i][d0]) = make_uint2(kw[i][0], kw[i][1]);
         } else {
           *reinterpret_cast<uint32_t*>(&Ks[buf][4 * kg + i][d0]) = kw[i][0];
+        }
+      }
+      if constexpr (KLO && P != SI_PREC_FP16) {  // fp16 rows are exact in fp16: no low part
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (DPT == 8) {
+            *reinterpret_cast<uint4*>(&Kls[buf][4 * kg + i][d0]) =
+                make_uint4(kl[i][0], kl[i][1], kl[i][2], kl[i][3]);
+          } else if constexpr (DPT == 4) {
+            *reinterpret_cast<uint2*>(&Kls[buf][4 * kg + i][d0]) = make_uint2(kl[i][0], kl[i][1]);
+          } else {
+            *reinterpret_cast<uint32_t*>(&Kls[buf][4 * kg + i][d0]) = kl[i][0];
+          }
         }
       }
       // V rows like K rows (tile_pv reads them transposed)
@@ -831,10 +884,12 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
   };
 
   // S^T = K Q^T, online softmax and O^T += V^T P^T for the tile in buffer buf.
-  auto compute_tile = [&](int nv, int buf) __attribute__((always_inline)) {
+  auto compute_tile = [&](auto PC, int nv, int buf) __attribute__((always_inline)) {
+    constexpr int P = decltype(PC)::value;
     v16f sacc[2];
     uint32_t pw[16];
     tile_qk<D>(Ks[buf], qf, col, grp, cinit, sacc);
+    if constexpr (KLO && P != SI_PREC_FP16) tile_qk_lo<D>(Kls[buf], qf, col, grp, sacc);
     tile_softmax<D>(sacc, nv, grp, m_run, cinit, l_run, o, pw);
     tile_pv<D>(Vs[buf], pw, col, grp, o);
     __builtin_amdgcn_s_setprio(0);
@@ -900,7 +955,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
     lds_barrier();
     // All tiles but the last; the loop body has no branch over loads in flight.
     for (int tt = t0; tt < t1 - 1; ++tt) {
-      compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(tt, P)), buf);
+      compute_tile(PC, __builtin_amdgcn_readfirstlane(tile_valid(tt, P)), buf);
       // Decode the next tile into the other buffer, then prefetch.
       decode_tile(PC, min(tt + 1, t_last), buf ^ 1);
       fetch_data(PC, tt + 2);
@@ -928,7 +983,7 @@ __global__ __launch_bounds__(512) void attn_packed_fwd(
       const int i2 = min(min(t1 + 1, nl), max(tstart[4] - 1, 0));
       sl_n2 = *reinterpret_cast<const int4*>(lh + (int64_t)i2 * BN + 4 * kg);
     }
-    compute_tile(__builtin_amdgcn_readfirstlane(tile_valid(t_last, P)), buf);
+    compute_tile(PC, __builtin_amdgcn_readfirstlane(tile_valid(t_last, P)), buf);
     prefetch_next(PC);
     lds_barrier();  // also frees the tile buffers for the output staging
     buf ^= 1;

@@ -49,6 +49,26 @@ def test_attention_small_vs_oracle(dev, qdtype, B, H, Sq, Skv, D):
     assert _rel_l2(out.float().cpu(), ref) <= TOL
 
 
+@pytest.mark.parametrize("D,qdtype,g", [(64, torch.float16, 8), (64, torch.bfloat16, 16),
+                                        (128, torch.float16, 16), (128, torch.bfloat16, 8)])
+def test_attention_fp32_inputs_outlier_channels(dev, D, qdtype, g):
+    """fp32 K/V with 5% outlier channels (x8) and queries at 1.5 sigma, every
+    precision present: peaked scores, where K rounded to fp16 is most of the
+    error (8.1-8.6e-4 on these cases; up to 1.25e-3 in a random sweep of such
+    inputs). Caches of fp32 inputs carry K as fp16 hi + lo, which leaves Q's
+    and P's fp16 rounding (4.2-4.7e-4 here), so they are held to 6e-4."""
+    B, H, Sq, Skv = 2, 2, 600, 1400
+    k, v = kv_inputs(B, H, Skv, D, torch.float32, seed=D + g, outlier_frac=0.05)
+    codes = mixed_codes(Skv, H, seed=D * g, probs=(1, 1, 1, 1), sink=4, evicted=0.1)
+    cache = _pack(k, v, codes, dev, group_size=g)
+    q = (torch.randn(B, H, Sq, D, generator=torch.Generator().manual_seed(D - g)) * 1.5).to(qdtype)
+    out = packed_attention(q.to(dev), cache)
+    rk, rv = O.kv_unpack(oracle_pack(k, v, codes, group_size=g))
+    ref = O.attention(q.float().numpy().reshape(B * H, Sq, D), rk.reshape(B * H, Skv, D),
+                      rv.reshape(B * H, Skv, D)).reshape(B, H, Sq, D)
+    assert _rel_l2(out.float().cpu(), ref) <= 6e-4
+
+
 def _dense_reference(q, k, v):
     """float64 softmax(q k^T / sqrt(D)) v on the device, one head at a time."""
     B, H, Sq, D = q.shape
